@@ -1,0 +1,111 @@
+/*
+ * pmkl_attn.h - C ABI of the MI355X (gfx950) fused causal self-attention forward.
+ *
+ * This is the drop-in boundary for the pmkl hot path.  Every entry point takes
+ * plain pointers and sizes; no C++, HIP or torch type crosses it (the stream is
+ * passed as an opaque hipStream_t cast to void*).
+ *
+ * Interfaces replaced:
+ *   pmkl::nlp::causal_attention_forward<scalar_t, BLOCK_M, HIDDEN_SIZE>(
+ *       out, q, k, v, batch_size, num_heads, seq_length, out_m, out_l)
+ *       -> reference pmkl/nlp/causal_attention.h:258-288
+ *   fused_self_attention_fw(q, k, v, is_causal) -> (out, out_m, out_l)
+ *       -> reference pmkl_pytorch_ext/fused_self_attention.cpp:139-173
+ *
+ * Semantics (identical to the reference CPU operator,
+ * fused_self_attention.cpp:5-64, evaluated with fp32 accumulation):
+ *   s_ij = scale * <q_i, k_j>           (scale defaults to 1.0f/sqrtf((float)D))
+ *   s_ij = -inf for j > i when causal
+ *   m_i  = max_j s_ij
+ *   l_i  = sum_j exp(s_ij - m_i)        (a plain sum, not a log-sum-exp)
+ *   o_i  = sum_j exp(s_ij - m_i) / l_i * v_j
+ * Tensors are [batch, heads, seq, head_dim] with head_dim contiguous; m and l
+ * are contiguous [batch, heads, seq].
+ *
+ * Contract:
+ *   - The caller allocates q, k, v, o, m, l in device memory; the library
+ *     allocates nothing per call.
+ *   - Calls are asynchronous on the given stream (NULL = the default stream).
+ *   - The functions are re-entrant and thread-safe; error text is thread-local.
+ */
+#ifndef PMKL_ATTN_H_
+#define PMKL_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PMKL_ABI_VERSION 1
+
+/* Element types.  The reference dispatches on float, double, half and
+ * bfloat16 (fused_self_attention.cpp:152-156); the device path implements
+ * float, half and bfloat16.  double stays on the CPU branch of the torch op. */
+typedef enum pmkl_dtype {
+    PMKL_DTYPE_F32 = 0,
+    PMKL_DTYPE_F16 = 1,
+    PMKL_DTYPE_BF16 = 2
+} pmkl_dtype;
+
+/* Status codes.  The reference raises pmkl::utils::Error from CHECK_FAIL
+ * (pmkl/core/utils/exception.h:121-161); at the C boundary that becomes a
+ * status code plus pmkl_last_error() text. */
+typedef enum pmkl_status {
+    PMKL_OK = 0,
+    PMKL_EINVAL = 1,      /* bad shape, null pointer, misalignment, bad stride */
+    PMKL_EUNSUPPORTED = 2,/* no compiled kernel for this dtype / head_dim      */
+    PMKL_EHIP = 3         /* the HIP runtime reported an error at launch        */
+} pmkl_status;
+
+/* Arguments of pmkl_attn_fwd.  Strides are in elements; a zero stride triple
+ * means "contiguous [B, H, S, D]".  head_dim is always contiguous. */
+typedef struct pmkl_attn_fwd_args {
+    const void *q;
+    const void *k;
+    const void *v;
+    void *o;
+    void *m;            /* [B, H, S] row max of the scaled, masked logits       */
+    void *l;            /* [B, H, S] sum_j exp(s_ij - m_i)                       */
+    int32_t dtype;      /* pmkl_dtype of q, k, v, o                              */
+    int32_t ml_dtype;   /* pmkl_dtype of m and l: dtype (as the reference) or F32 */
+    int64_t batch;
+    int64_t heads;
+    int64_t seq_len;
+    int64_t head_dim;   /* 32, 64 or 128                                          */
+    int64_t q_strides[3]; /* batch, head, seq strides (elements)                  */
+    int64_t k_strides[3];
+    int64_t v_strides[3];
+    int64_t o_strides[3];
+    float scale;        /* 0 -> 1.0f / sqrtf((float)head_dim)                     */
+    int32_t is_causal;  /* nonzero: lower-triangular mask j <= i                  */
+} pmkl_attn_fwd_args;
+
+/* General entry point.  Replaces the device half of fused_self_attention_fw
+ * (fused_self_attention.cpp:139-173): any seq_len >= 0, causal or not,
+ * strided q/k/v/o.  Returns a pmkl_status. */
+int pmkl_attn_fwd(const pmkl_attn_fwd_args *args, void *stream);
+
+/* Flat form of pmkl::nlp::causal_attention_forward (causal_attention.h:258-262):
+ * contiguous [B, H, S, D] tensors, causal mask, scale 1/sqrt(D), m and l in
+ * the tensor dtype.  Asynchronous on `stream`. */
+int pmkl_causal_attention_forward(int32_t dtype, void *out, const void *q, const void *k,
+                                  const void *v, int32_t batch_size, int32_t num_heads,
+                                  int32_t seq_length, int32_t hidden_size, void *out_m,
+                                  void *out_l, void *stream);
+
+/* 1 if a kernel is compiled for (dtype, head_dim), else 0. */
+int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim);
+
+/* Thread-local text of the last error ("" if none), with the file:line of the
+ * check that failed, in the style of the reference's CHECK_FAIL message. */
+const char *pmkl_last_error(void);
+
+/* PMKL_ABI_VERSION of the loaded library. */
+int pmkl_abi_version(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* PMKL_ATTN_H_ */

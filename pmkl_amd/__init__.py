@@ -1,0 +1,66 @@
+"""pmkl_amd - MI355X (gfx950) fused causal self-attention forward.
+
+Drop-in replacement for pmkl's attention path:
+  * C++:    include/pmkl/nlp/causal_attention.h  (pmkl::nlp::causal_attention_forward)
+  * C ABI:  include/pmkl_attn.h                  (libpmkl_attn.so)
+  * torch:  pmkl_amd.pmkl_pytorch_ext.fused_self_attention_fw
+  * Python: pmkl_amd.pmkl_function.fused_self_attention
+
+`attn_fwd` below calls the C ABI directly on device tensors through ctypes;
+it is what the parity tests and the benchmark use.
+"""
+from __future__ import annotations
+
+from . import capi
+
+__all__ = ["attn_fwd", "capi", "torch_dtype_to_pmkl"]
+
+
+def torch_dtype_to_pmkl(dt) -> int:
+    import torch
+
+    table = {torch.float32: capi.PMKL_DTYPE_F32, torch.float16: capi.PMKL_DTYPE_F16,
+             torch.bfloat16: capi.PMKL_DTYPE_BF16}
+    if dt not in table:
+        raise TypeError(f"unsupported dtype {dt} (float32, float16, bfloat16)")
+    return table[dt]
+
+
+def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dtype=None,
+             out=None, out_m=None, out_l=None, stream=None):
+    """Fused attention forward on ROCm tensors [B, H, S, D] through pmkl_attn_fwd.
+
+    Returns (out, out_m, out_l).  out is contiguous [B, H, S, D] in q's dtype;
+    out_m / out_l are [B, H, S] in `ml_dtype` (default: q's dtype, as the
+    reference operator).  q, k, v may be strided as long as head_dim is
+    contiguous.  Runs on `stream` (a raw hipStream_t int) or torch's current
+    stream; nothing is synchronised.
+    """
+    import torch
+
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("attn_fwd takes ROCm device tensors")
+    if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, v must share a 4-D shape [B, H, S, D]")
+    B, H, S, D = q.shape
+    dt = torch_dtype_to_pmkl(q.dtype)
+    mdt = q.dtype if ml_dtype is None else ml_dtype
+    if out is None:
+        out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    if out_m is None:
+        out_m = torch.empty((B, H, S), dtype=mdt, device=q.device)
+    if out_l is None:
+        out_l = torch.empty((B, H, S), dtype=mdt, device=q.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    a = capi.make_args(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), out_m.data_ptr(),
+                       out_l.data_ptr(), dtype=dt, ml_dtype=torch_dtype_to_pmkl(mdt), batch=B, heads=H,
+                       seq_len=S, head_dim=D, is_causal=is_causal, scale=0.0 if scale is None else float(scale),
+                       q_strides=q.stride()[:3], k_strides=k.stride()[:3], v_strides=v.stride()[:3],
+                       o_strides=out.stride()[:3])
+    if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1 or out.stride(3) != 1:
+        raise ValueError("head_dim must be contiguous")
+    rc = capi.attn_fwd_raw(a, stream)
+    if rc != capi.PMKL_OK:
+        raise capi.PmklError(rc, capi.last_error())
+    return out, out_m, out_l

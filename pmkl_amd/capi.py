@@ -1,0 +1,121 @@
+"""ctypes view of the C ABI in include/pmkl_attn.h (libpmkl_attn.so).
+
+This is the thin Python handle on the drop-in boundary: it passes device
+pointers, sizes and a HIP stream, nothing else.  Loading fails loudly when the
+library has not been built; there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+_LIB_PATH = Path(__file__).resolve().parent / "libpmkl_attn.so"
+
+PMKL_DTYPE_F32 = 0
+PMKL_DTYPE_F16 = 1
+PMKL_DTYPE_BF16 = 2
+
+PMKL_OK = 0
+PMKL_EINVAL = 1
+PMKL_EUNSUPPORTED = 2
+PMKL_EHIP = 3
+
+# Every symbol include/pmkl_attn.h declares.
+EXPORTED_SYMBOLS = (
+    "pmkl_attn_fwd",
+    "pmkl_causal_attention_forward",
+    "pmkl_attn_fwd_supported",
+    "pmkl_last_error",
+    "pmkl_abi_version",
+)
+
+
+class AttnFwdArgs(ctypes.Structure):
+    """Mirror of pmkl_attn_fwd_args."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("m", ctypes.c_void_p),
+        ("l", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ml_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("q_strides", ctypes.c_int64 * 3),
+        ("k_strides", ctypes.c_int64 * 3),
+        ("v_strides", ctypes.c_int64 * 3),
+        ("o_strides", ctypes.c_int64 * 3),
+        ("scale", ctypes.c_float),
+        ("is_causal", ctypes.c_int32),
+    ]
+
+
+class PmklError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"pmkl error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libpmkl_attn.so (raises if it is missing)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not _LIB_PATH.exists():
+        raise ImportError(f"{_LIB_PATH} is not built; run __graft_entry__.build() or python -m pmkl_amd._build")
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    lib.pmkl_attn_fwd.argtypes = [ctypes.POINTER(AttnFwdArgs), ctypes.c_void_p]
+    lib.pmkl_attn_fwd.restype = ctypes.c_int
+    lib.pmkl_causal_attention_forward.argtypes = [
+        ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+    ]
+    lib.pmkl_causal_attention_forward.restype = ctypes.c_int
+    lib.pmkl_attn_fwd_supported.argtypes = [ctypes.c_int32, ctypes.c_int64]
+    lib.pmkl_attn_fwd_supported.restype = ctypes.c_int
+    lib.pmkl_last_error.argtypes = []
+    lib.pmkl_last_error.restype = ctypes.c_char_p
+    lib.pmkl_abi_version.argtypes = []
+    lib.pmkl_abi_version.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def last_error() -> str:
+    return load().pmkl_last_error().decode()
+
+
+def attn_fwd_raw(args: AttnFwdArgs, stream: int | None = None) -> int:
+    """Call pmkl_attn_fwd; returns the status code."""
+    return load().pmkl_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream or 0))
+
+
+def make_args(q, k, v, o, m, l, *, dtype: int, ml_dtype: int | None = None, batch: int, heads: int,
+              seq_len: int, head_dim: int, is_causal: bool = True, scale: float = 0.0,
+              q_strides=(0, 0, 0), k_strides=(0, 0, 0), v_strides=(0, 0, 0), o_strides=(0, 0, 0)) -> AttnFwdArgs:
+    """Build an AttnFwdArgs from raw integer pointers."""
+    a = AttnFwdArgs()
+    a.q, a.k, a.v, a.o, a.m, a.l = q, k, v, o, m, l
+    a.dtype = dtype
+    a.ml_dtype = dtype if ml_dtype is None else ml_dtype
+    a.batch, a.heads, a.seq_len, a.head_dim = batch, heads, seq_len, head_dim
+    a.q_strides[:] = list(q_strides)
+    a.k_strides[:] = list(k_strides)
+    a.v_strides[:] = list(v_strides)
+    a.o_strides[:] = list(o_strides)
+    a.scale = scale
+    a.is_causal = 1 if is_causal else 0
+    return a

@@ -1,0 +1,220 @@
+// C ABI of the gfx950 fused causal self-attention forward (include/pmkl_attn.h).
+//
+// Host side of the path: argument validation, kernel selection and launch.
+// It replaces the reference launcher pmkl::nlp::causal_attention_forward
+// (pmkl/nlp/causal_attention.h:258-288), which checks S % 32 and the shared
+// memory size with CHECK_FAIL and submits one lambda through the CUDA/SYCL
+// GpuLauncher singleton (pmkl/core/launcher/cuda_launcher.h:297-335).  Here a
+// named __global__ kernel is launched directly on the caller's stream, launch
+// errors are checked (the reference never calls cudaGetLastError), and errors
+// come back as status codes with thread-local text instead of exceptions.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/pmkl_attn.h"
+#include "attn_fwd_kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *file, int line, const char *fmt, ...) {
+    char msg[400];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof(msg), fmt, ap);
+    va_end(ap);
+    const char *base = strrchr(file, '/');
+    snprintf(g_err, sizeof(g_err), "[pmkl check failed at %s:%d] %s", base ? base + 1 : file, line, msg);
+    return code;
+}
+
+#define PMKL_FAIL(code, ...) return fail((code), __FILE__, __LINE__, __VA_ARGS__)
+#define PMKL_REQUIRE(cond, code, ...) \
+    do {                              \
+        if (!(cond)) PMKL_FAIL((code), __VA_ARGS__); \
+    } while (0)
+
+size_t dtype_size(int32_t dt) { return dt == PMKL_DTYPE_F32 ? 4 : 2; }
+
+bool dtype_valid(int32_t dt) {
+    return dt == PMKL_DTYPE_F32 || dt == PMKL_DTYPE_F16 || dt == PMKL_DTYPE_BF16;
+}
+
+bool head_dim_supported(int64_t d) { return d == 32 || d == 64 || d == 128; }
+
+using pmkl_amd::AttnParams;
+typedef void (*kernel_fn)(AttnParams);
+
+template <typename T, int D>
+kernel_fn pick16(bool causal) {
+    return causal ? (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, true>
+                  : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false>;
+}
+template <int D>
+kernel_fn pick32(bool causal) {
+    return causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, true>
+                  : (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, false>;
+}
+
+kernel_fn select_kernel(int32_t dt, int64_t d, bool causal) {
+    switch (dt) {
+        case PMKL_DTYPE_BF16:
+            if (d == 32) return pick16<__bf16, 32>(causal);
+            if (d == 64) return pick16<__bf16, 64>(causal);
+            if (d == 128) return pick16<__bf16, 128>(causal);
+            break;
+        case PMKL_DTYPE_F16:
+            if (d == 32) return pick16<_Float16, 32>(causal);
+            if (d == 64) return pick16<_Float16, 64>(causal);
+            if (d == 128) return pick16<_Float16, 128>(causal);
+            break;
+        case PMKL_DTYPE_F32:
+            if (d == 32) return pick32<32>(causal);
+            if (d == 64) return pick32<64>(causal);
+            if (d == 128) return pick32<128>(causal);
+            break;
+        default:
+            break;
+    }
+    return nullptr;
+}
+
+// Fills the three strides with the contiguous [B, H, S, D] ones when all are zero.
+void default_strides(int64_t st[3], const int64_t in[3], int64_t H, int64_t S, int64_t D) {
+    if (in[0] == 0 && in[1] == 0 && in[2] == 0) {
+        st[0] = H * S * D;
+        st[1] = S * D;
+        st[2] = D;
+    } else {
+        st[0] = in[0];
+        st[1] = in[1];
+        st[2] = in[2];
+    }
+}
+
+int check_tensor(const char *name, const void *ptr, const int64_t st[3], int64_t B, int64_t H, int64_t S,
+                 int64_t D, size_t esize) {
+    const size_t vec = 16 / esize;  // elements per 16-byte access
+    PMKL_REQUIRE(ptr != nullptr, PMKL_EINVAL, "%s is a null pointer", name);
+    PMKL_REQUIRE(((uintptr_t)ptr % 16) == 0, PMKL_EINVAL, "%s must be 16-byte aligned", name);
+    PMKL_REQUIRE(st[0] >= 0 && st[1] >= 0 && st[2] >= D, PMKL_EINVAL,
+                 "%s strides (%lld, %lld, %lld) must be non-negative with seq stride >= head_dim %lld", name,
+                 (long long)st[0], (long long)st[1], (long long)st[2], (long long)D);
+    PMKL_REQUIRE(st[0] % vec == 0 && st[1] % vec == 0 && st[2] % vec == 0, PMKL_EINVAL,
+                 "%s strides (%lld, %lld, %lld) must be multiples of %zu elements (16 bytes)", name,
+                 (long long)st[0], (long long)st[1], (long long)st[2], vec);
+    // The largest element offset must stay addressable with 64-bit arithmetic.
+    const double span = (double)(B - 1) * st[0] + (double)(H - 1) * st[1] + (double)(S - 1) * st[2] + D;
+    PMKL_REQUIRE(span < 9.0e18, PMKL_EINVAL, "%s spans too many elements", name);
+    return PMKL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *pmkl_last_error(void) { return g_err; }
+
+int pmkl_abi_version(void) { return PMKL_ABI_VERSION; }
+
+int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim) {
+    return dtype_valid(dtype) && head_dim_supported(head_dim) ? 1 : 0;
+}
+
+int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
+    g_err[0] = '\0';
+    PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
+    PMKL_REQUIRE(dtype_valid(a->dtype), PMKL_EUNSUPPORTED, "unsupported dtype %d", (int)a->dtype);
+    PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
+                 "ml_dtype %d must equal dtype %d or be F32", (int)a->ml_dtype, (int)a->dtype);
+    PMKL_REQUIRE(a->batch >= 0 && a->heads >= 0 && a->seq_len >= 0, PMKL_EINVAL,
+                 "negative shape (batch %lld, heads %lld, seq %lld)", (long long)a->batch, (long long)a->heads,
+                 (long long)a->seq_len);
+    PMKL_REQUIRE(head_dim_supported(a->head_dim), PMKL_EUNSUPPORTED,
+                 "head_dim %lld has no compiled kernel (supported: 32, 64, 128)", (long long)a->head_dim);
+    PMKL_REQUIRE(std::isfinite(a->scale) && a->scale >= 0.f, PMKL_EINVAL, "scale must be finite and >= 0");
+    // Empty problem: nothing to do (reference causal_attention.h:270).
+    if (a->batch * a->heads * a->seq_len == 0) return PMKL_OK;
+
+    const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
+    PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
+                 (long long)(B * H), (long long)S);
+    const int64_t n_qtiles = (S + pmkl_amd::kBlockM - 1) / pmkl_amd::kBlockM;
+    PMKL_REQUIRE(n_qtiles * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
+                 (long long)(n_qtiles * B * H));
+
+    const size_t es = dtype_size(a->dtype);
+    int64_t qs[3], ks[3], vs[3], os[3];
+    default_strides(qs, a->q_strides, H, S, D);
+    default_strides(ks, a->k_strides, H, S, D);
+    default_strides(vs, a->v_strides, H, S, D);
+    default_strides(os, a->o_strides, H, S, D);
+    int rc;
+    if ((rc = check_tensor("q", a->q, qs, B, H, S, D, es)) != PMKL_OK) return rc;
+    if ((rc = check_tensor("k", a->k, ks, B, H, S, D, es)) != PMKL_OK) return rc;
+    if ((rc = check_tensor("v", a->v, vs, B, H, S, D, es)) != PMKL_OK) return rc;
+    if ((rc = check_tensor("o", a->o, os, B, H, S, D, es)) != PMKL_OK) return rc;
+    PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
+    const size_t ml_es = dtype_size(a->ml_dtype);
+    PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
+                 "m / l must be aligned to their element size");
+
+    kernel_fn fn = select_kernel(a->dtype, D, a->is_causal != 0);
+    PMKL_REQUIRE(fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
+                 (long long)D);
+
+    AttnParams p;
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.m = a->m;
+    p.l = a->l;
+    p.q_sb = qs[0]; p.q_sh = qs[1]; p.q_ss = qs[2];
+    p.k_sb = ks[0]; p.k_sh = ks[1]; p.k_ss = ks[2];
+    p.v_sb = vs[0]; p.v_sh = vs[1]; p.v_ss = vs[2];
+    p.o_sb = os[0]; p.o_sh = os[1]; p.o_ss = os[2];
+    p.H = (int32_t)H;
+    p.S = (int32_t)S;
+    p.BH = (int32_t)(B * H);
+    p.n_qtiles = (int32_t)n_qtiles;
+    // Reference scale: 1.0f / std::sqrt((float)hidden_size), fused_self_attention.cpp:30.
+    p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
+    p.scale_log2 = p.scale * 1.4426950408889634f;
+    p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
+
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(n_qtiles * B * H)), dim3(pmkl_amd::kThreads), 0, st, p);
+    hipError_t err = hipGetLastError();
+    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return PMKL_OK;
+}
+
+int pmkl_causal_attention_forward(int32_t dtype, void *out, const void *q, const void *k, const void *v,
+                                  int32_t batch_size, int32_t num_heads, int32_t seq_length, int32_t hidden_size,
+                                  void *out_m, void *out_l, void *stream) {
+    pmkl_attn_fwd_args a;
+    memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = out;
+    a.m = out_m;
+    a.l = out_l;
+    a.dtype = dtype;
+    a.ml_dtype = dtype;
+    a.batch = batch_size;
+    a.heads = num_heads;
+    a.seq_len = seq_length;
+    a.head_dim = hidden_size;
+    a.scale = 0.f;
+    a.is_causal = 1;
+    return pmkl_attn_fwd(&a, stream);
+}
+
+}  // extern "C"

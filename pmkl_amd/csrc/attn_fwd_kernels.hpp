@@ -1,0 +1,483 @@
+// gfx950 (CDNA4) kernels of the fused causal self-attention forward.
+//
+// Reference path: pmkl/nlp/causal_attention.h:145-256 (GPU kernel) and
+// pmkl_pytorch_ext/fused_self_attention.cpp:5-64 (CPU operator).  The
+// reference kernel is scalar fp32 with ~2,250 block barriers per key tile; the
+// kernels here are written for wave64 MFMA instead:
+//
+//  * Scores are computed transposed, S^T = K * Q^T, with
+//    v_mfma_f32_32x32x16_{bf16,f16} (v_mfma_f32_32x32x2f32 for fp32).  In the
+//    32x32 accumulator layout a lane owns one query column and 16 key rows, so
+//    the row max and row sum of the softmax are in-lane reductions plus one
+//    v_permlane32_swap between the two lane halves.
+//  * K rows are fed to the MFMA A operand in a permuted order (pi below) so
+//    that lane half h ends up owning 16 consecutive keys.  Those 16 fp32
+//    probabilities, converted to bf16/fp16, are exactly the B operand of the
+//    P*V MFMA (O^T = V^T * P^T): P never goes through LDS.
+//  * V^T is read from a row-major V tile with ds_read_b64_tr_b16 (the gfx950
+//    LDS transpose read), so K and V share one staging scheme.
+//  * K/V tiles are double buffered in LDS with XOR swizzles chosen so that the
+//    MFMA operand reads are bank-conflict free; Q stays in VGPRs.
+//  * Key tiles wholly above the diagonal are never loaded or computed; the
+//    mask is applied element-wise only on tiles that straddle the diagonal or
+//    the end of the sequence.  Workgroups are issued longest-first.
+//  * Softmax is FA2-style: running max and per-lane partial sum, exp2 with
+//    scale*log2(e) folded into one FMA, normalisation once in the epilogue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pmkl_amd {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Kernel parameters.  Strides are in elements; head_dim is contiguous.
+struct AttnParams {
+    const void *q;
+    const void *k;
+    const void *v;
+    void *o;
+    void *m;
+    void *l;
+    int64_t q_sb, q_sh, q_ss;
+    int64_t k_sb, k_sh, k_ss;
+    int64_t v_sb, v_sh, v_ss;
+    int64_t o_sb, o_sh, o_ss;
+    int32_t H;           // heads
+    int32_t S;           // sequence length
+    int32_t BH;          // batch * heads
+    int32_t n_qtiles;    // ceil(S / BLOCK_M)
+    float scale;         // multiplies raw dot products
+    float scale_log2;    // scale * log2(e)
+    int32_t ml_f32;      // 1: m/l stored as float, 0: stored in the tensor dtype
+};
+
+constexpr int kWaves = 4;                // waves per workgroup
+constexpr int kThreads = kWaves * 64;    // 256
+constexpr int kBlockM = 32 * kWaves;     // query rows per workgroup (32 per wave)
+
+// ---------------------------------------------------------------------------
+// small device helpers
+// ---------------------------------------------------------------------------
+
+// Value of x in the other half of the wave (lane ^ 32), combined with op.
+// v_permlane32_swap(old=x, src=x) returns {x_lo|x_lo, x_hi|x_hi}; so
+// max/sum of the two results is max/sum of x and its partner in every lane.
+__device__ __forceinline__ float half_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Row of the K tile fed to MFMA A-row i (0..31) of a 32-key block.  A-row
+// i = 8g + 4h + t lands in accumulator register 4g + t of lane half h, so
+// feeding it key 16h + 4g + t gives lane half h the keys 16h .. 16h+15 in
+// register order.
+__device__ __forceinline__ int key_of_arow(int i) {
+    return ((i >> 2) & 1) * 16 + (i >> 3) * 4 + (i & 3);
+}
+
+// 16-bit element traits: MFMA, and fp32 -> T packing.
+template <typename T> struct Elt16;
+template <> struct Elt16<__bf16> {
+    typedef bf16x8_t frag;
+    static __device__ __forceinline__ f32x16_t mma(frag a, frag b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        bf16x2_t v = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+};
+template <> struct Elt16<_Float16> {
+    typedef f16x8_t frag;
+    static __device__ __forceinline__ f32x16_t mma(frag a, frag b, f32x16_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+        f16x2_t v = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+};
+
+// XOR swizzles of the 16-byte chunks of a K / V tile row (CPR chunks per
+// row).  K is read with ds_read_b128 by the 32 A-rows in key_of_arow order;
+// V is read with ds_read_b64_tr_b16 by groups of 4 consecutive rows.
+template <int CPR> __device__ __forceinline__ int swz_k(int row) {
+    if constexpr (CPR >= 16) {
+        return (row & 3) | (((row >> 4) & 1) << 2) | (((row >> 2) & 1) << 3);
+    } else if constexpr (CPR == 8) {
+        return ((row >> 1) & 1) | (((row >> 4) & 1) << 1) | (((row >> 2) & 1) << 2);
+    } else {
+        return ((row >> 4) & 1) | (((row >> 2) & 1) << 1);
+    }
+}
+template <int CPR> __device__ __forceinline__ int swz_v(int row) {
+    if constexpr (CPR >= 16) {
+        return ((row & 3) << 1) | ((row & 1) << 3);
+    } else if constexpr (CPR == 8) {
+        return ((row >> 1) & 1) << 2;
+    } else {
+        return 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit kernel (bf16 / fp16), head_dim D in {32, 64, 128}
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams p) {
+    using E = Elt16<T>;
+    using frag = typename E::frag;
+    constexpr int BN = 64;                  // keys per tile
+    constexpr int CPR = D / 8;              // 16-byte chunks per row
+    constexpr int TILE_CHUNKS = BN * CPR;   // chunks per K (or V) tile
+    constexpr int LOADS = TILE_CHUNKS / kThreads;
+    constexpr int NDB = D / 32;             // 32-wide blocks of head_dim
+    constexpr int NDK = D / 16;             // 16-deep MFMA steps over head_dim
+    static_assert(TILE_CHUNKS % kThreads == 0, "tile not divisible by threads");
+
+    __shared__ __attribute__((aligned(16))) T smem[2][2][BN * D];  // [stage][K,V]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;          // lane half
+    const int col = lane & 31;         // query column owned by this lane
+
+    // Longest-first order: blockIdx.x walks all heads of the last query tile
+    // first.  Consecutive blocks of one head are BH apart, which keeps one
+    // head on one XCD when BH is a multiple of 8.
+    const int L = blockIdx.x;
+    const int bh = L % p.BH;
+    const int qt = CAUSAL ? (p.n_qtiles - 1 - L / p.BH) : (L / p.BH);
+    const int b = bh / p.H;
+    const int h = bh - b * p.H;
+    const int S = p.S;
+
+    const T *qg = (const T *)p.q + b * p.q_sb + h * p.q_sh;
+    const T *kg = (const T *)p.k + b * p.k_sb + h * p.k_sh;
+    const T *vg = (const T *)p.v + b * p.v_sb + h * p.v_sh;
+    T *og = (T *)p.o + b * p.o_sb + h * p.o_sh;
+
+    const int q0 = qt * kBlockM;
+    const int q0w = q0 + 32 * wave;
+    const int qi = q0w + col;                         // this lane's query row
+    const int last_key = CAUSAL ? min(q0 + kBlockM - 1, S - 1) : S - 1;
+    const int nt = last_key / BN + 1;                 // key tiles for the workgroup
+    const bool wave_active = q0w < S;
+
+    // Q fragments (B operand of S^T = K Q^T): lane holds Q[qi][16dk + 8hi .. +7].
+    frag qf[NDK];
+    {
+        const int qrow = min(qi, S - 1);
+        const T *src = qg + (int64_t)qrow * p.q_ss + 8 * hi;
+#pragma unroll
+        for (int dk = 0; dk < NDK; ++dk)
+            qf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(src + 16 * dk));
+    }
+
+    // Global -> register staging of one K/V tile.  Thread tid owns physical
+    // chunk slots j*256 + tid; it fetches the logical chunk that the swizzle
+    // places there.  Rows past the end of the sequence re-read row S-1 (finite
+    // data; those keys are masked).
+    u32x4_t kreg[LOADS], vreg[LOADS];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int sl = j * kThreads + tid;
+            const int row = sl / CPR;
+            const int pc = sl % CPR;
+            const int key = min(kt * BN + row, S - 1);
+            kreg[j] = *(const u32x4_t *)(kg + (int64_t)key * p.k_ss + 8 * (pc ^ swz_k<CPR>(row)));
+            vreg[j] = *(const u32x4_t *)(vg + (int64_t)key * p.v_ss + 8 * (pc ^ swz_v<CPR>(row)));
+        }
+    };
+    auto swrite = [&](int st) {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int sl = j * kThreads + tid;
+            *(u32x4_t *)(&smem[st][0][sl * 8]) = kreg[j];
+            *(u32x4_t *)(&smem[st][1][sl * 8]) = vreg[j];
+        }
+    };
+
+    f32x16_t acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    float m_run = -INFINITY;   // running row max, raw dot-product units
+    float l_run = 0.f;         // per-lane partial row sum relative to m_run
+
+    // Per-lane constant parts of the LDS addresses.
+    const int arow = key_of_arow(col);        // K tile row read by this lane (per 32-key block)
+    const int g = lane >> 4, tt = lane & 15;  // 16-lane group for the V transpose read
+    const int vrow0 = 16 * (g >> 1) + (tt >> 2);
+    const int vcol0 = 16 * (g & 1) + 4 * (tt & 3);
+
+    gload(0);
+    swrite(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < nt; ++kt) {
+        const int st = kt & 1;
+        if (kt + 1 < nt) gload(kt + 1);
+        const int kbase = kt * BN;
+        const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
+        if (wave_needed) {
+            const T *Ks = smem[st][0];
+            const T *Vs = smem[st][1];
+            // ---- S^T = K Q^T for two 32-key blocks ----
+            f32x16_t sacc[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+                const int row = 32 * kb + arow;
+                const T *krow = Ks + row * D;
+                const int sw = swz_k<CPR>(row);
+#pragma unroll
+                for (int dk = 0; dk < NDK; ++dk) {
+                    const int x = 2 * dk + hi;
+                    frag a = __builtin_bit_cast(frag, *(const u32x4_t *)(krow + 8 * (x ^ sw)));
+                    sacc[kb] = E::mma(a, qf[dk], sacc[kb]);
+                }
+            }
+            // ---- mask (only tiles that straddle the diagonal or the end) ----
+            const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+            if (need_mask) {
+                const int lim = CAUSAL ? min(qi, S - 1) : S - 1;   // last visible key
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kbase + 32 * kb + 16 * hi + r;
+                        if (key > lim) sacc[kb][r] = -INFINITY;
+                    }
+            }
+            // ---- online softmax ----
+            float mx = sacc[0][0];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+            mx = half_max(mx);
+            const float m_new = fmaxf(m_run, mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = fast_exp2((m_run - m_use) * p.scale_log2);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+            const float moff = -m_use * p.scale_log2;
+            uint32_t pk[2][8];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const float p0 = fast_exp2(__builtin_fmaf(sacc[kb][r], p.scale_log2, moff));
+                    const float p1 = fast_exp2(__builtin_fmaf(sacc[kb][r + 1], p.scale_log2, moff));
+                    l_run += p0 + p1;
+                    pk[kb][r >> 1] = E::pack2(p0, p1);
+                }
+            // ---- O^T += V^T P^T ----
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    u32x4_t bw = {pk[kb][4 * c], pk[kb][4 * c + 1], pk[kb][4 * c + 2], pk[kb][4 * c + 3]};
+                    const frag bfr = __builtin_bit_cast(frag, bw);
+                    const int r0 = 32 * kb + 8 * c + vrow0;      // rows r0 .. (elements 0-3), r0+4 .. (4-7)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        const int cc = 32 * db + vcol0;             // element column of this lane's 4-wide read
+                        const int ch = cc >> 3, part = cc & 7;
+                        const T *a0 = Vs + r0 * D + 8 * (ch ^ swz_v<CPR>(r0)) + part;
+                        const T *a1 = Vs + (r0 + 4) * D + 8 * (ch ^ swz_v<CPR>(r0 + 4)) + part;
+                        typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+                        s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a0);
+                        s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a1);
+                        typedef short s16x8_t __attribute__((ext_vector_type(8)));
+                        s16x8_t a8 = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                        acc[db] = E::mma(__builtin_bit_cast(frag, a8), bfr, acc[db]);
+                    }
+                }
+        }
+        if (kt + 1 < nt) swrite(st ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: normalise, store O, m, l ----
+    const float l_tot = half_sum(l_run);
+    if (wave_active && qi < S) {
+        const float inv = 1.0f / l_tot;
+        T *orow = og + (int64_t)qi * p.o_ss;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * db + 8 * g4 + 4 * hi;
+                u32x2_t w2 = {E::pack2(acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv),
+                              E::pack2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv)};
+                *(u32x2_t *)(orow + d) = w2;
+            }
+        if (hi == 0) {
+            const int64_t mi = (int64_t)bh * S + qi;
+            const float mval = m_run * p.scale;
+            if (p.ml_f32) {
+                ((float *)p.m)[mi] = mval;
+                ((float *)p.l)[mi] = l_tot;
+            } else {
+                ((T *)p.m)[mi] = (T)mval;
+                ((T *)p.l)[mi] = (T)l_tot;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 kernel (true fp32 arithmetic on v_mfma_f32_32x32x2f32), D in {32,64,128}
+// ---------------------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(AttnParams p) {
+    constexpr int BN = 32;           // keys per tile
+    constexpr int LD = D + 1;        // padded LDS row (floats)
+    constexpr int NDB = D / 32;
+    constexpr int NDK = D / 2;
+    __shared__ float Ks[BN * LD];
+    __shared__ float Vs[BN * LD];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int col = lane & 31;
+
+    const int L = blockIdx.x;
+    const int bh = L % p.BH;
+    const int qt = CAUSAL ? (p.n_qtiles - 1 - L / p.BH) : (L / p.BH);
+    const int b = bh / p.H;
+    const int h = bh - b * p.H;
+    const int S = p.S;
+
+    const float *qg = (const float *)p.q + b * p.q_sb + h * p.q_sh;
+    const float *kg = (const float *)p.k + b * p.k_sb + h * p.k_sh;
+    const float *vg = (const float *)p.v + b * p.v_sb + h * p.v_sh;
+    float *og = (float *)p.o + b * p.o_sb + h * p.o_sh;
+
+    const int q0 = qt * kBlockM;
+    const int q0w = q0 + 32 * wave;
+    const int qi = q0w + col;
+    const int last_key = CAUSAL ? min(q0 + kBlockM - 1, S - 1) : S - 1;
+    const int nt = last_key / BN + 1;
+    const bool wave_active = q0w < S;
+
+    float qf[NDK];
+    {
+        const int qrow = min(qi, S - 1);
+        const float *src = qg + (int64_t)qrow * p.q_ss + hi;
+#pragma unroll
+        for (int dk = 0; dk < NDK; ++dk) qf[dk] = src[2 * dk];
+    }
+
+    f32x16_t acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const int arow = key_of_arow(col);
+
+    for (int kt = 0; kt < nt; ++kt) {
+        const int kbase = kt * BN;
+        for (int i = tid; i < BN * D; i += kThreads) {
+            const int r = i / D, c = i % D;
+            const int key = min(kbase + r, S - 1);
+            Ks[r * LD + c] = kg[(int64_t)key * p.k_ss + c];
+            Vs[r * LD + c] = vg[(int64_t)key * p.v_ss + c];
+        }
+        __syncthreads();
+        const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
+        if (wave_needed) {
+            f32x16_t sacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+#pragma unroll
+            for (int dk = 0; dk < NDK; ++dk)
+                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[arow * LD + 2 * dk + hi], qf[dk], sacc, 0, 0, 0);
+            const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+            if (need_mask) {
+                const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kbase + 16 * hi + r > lim) sacc[r] = -INFINITY;
+            }
+            float mx = sacc[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+            mx = half_max(mx);
+            const float m_new = fmaxf(m_run, mx);
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float alpha = fast_exp2((m_run - m_use) * p.scale_log2);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+            const float moff = -m_use * p.scale_log2;
+            float pr[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                pr[r] = fast_exp2(__builtin_fmaf(sacc[r], p.scale_log2, moff));
+                l_run += pr[r];
+            }
+#pragma unroll
+            for (int c = 0; c < 16; ++c)
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(16 * hi + c) * LD + 32 * db + col], pr[c],
+                                                                    acc[db], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    const float l_tot = half_sum(l_run);
+    if (wave_active && qi < S) {
+        const float inv = 1.0f / l_tot;
+        float *orow = og + (int64_t)qi * p.o_ss;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * db + 8 * g4 + 4 * hi;
+                float4 w4 = {acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv, acc[db][4 * g4 + 2] * inv,
+                             acc[db][4 * g4 + 3] * inv};
+                *(float4 *)(orow + d) = w4;
+            }
+        if (hi == 0) {
+            const int64_t mi = (int64_t)bh * S + qi;
+            ((float *)p.m)[mi] = m_run * p.scale;
+            ((float *)p.l)[mi] = l_tot;
+        }
+    }
+}
+
+}  // namespace pmkl_amd

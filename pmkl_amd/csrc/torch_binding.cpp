@@ -1,0 +1,171 @@
+// pmkl_pytorch_ext: the PyTorch-ROCm operator of the fused self-attention
+// forward, rebuilt as a binding over the C ABI in include/pmkl_attn.h.
+//
+// Replaces pmkl_pytorch_ext/fused_self_attention.cpp:139-173 and :217-220 of
+// the reference (same module name, function name, arguments, return tuple and
+// TORCH_CHECK messages).  The reference has only a CPU body; this binding
+//   * sends tensors on a ROCm device to pmkl_attn_fwd (the gfx950 kernels), on
+//     the current HIP stream, with no host synchronisation;
+//   * keeps the CPU body for CPU tensors: host_attention_forward below computes
+//     exactly what the reference CPU operator computes (same per-element
+//     operation sequence in scalar_t, so c10 Half/BFloat16 round after every
+//     operation and the softmax denominator is accumulated in double), with the
+//     heads spread over at::parallel_for threads.  Device tensors never reach it.
+// Outputs are allocated contiguous [B, H, S, D] (the reference uses
+// empty_like(v), which keeps a strided v's layout while the body writes it as
+// if it were contiguous); out_m and out_l are [B, H, S] in v's dtype.
+#include <torch/extension.h>
+
+#include <ATen/Parallel.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cmath>
+#include <limits>
+
+#include "../../include/pmkl_attn.h"
+
+namespace {
+
+// CPU body.  Per head b and query row i, the same steps as the reference
+// (fused_self_attention.cpp:13-63): full-length score row in scalar_t,
+// -inf mask, max, double denominator, p = exp(s - max) / e2sum rounded to
+// scalar_t, then o_i = sum_j p_ij v_j accumulated in scalar_t in key order.
+// The row is kept in a length-S buffer instead of an S x S matrix, and the PV
+// sum walks keys in the outer loop; every output element still sees the same
+// operations in the same order.
+template <typename scalar_t>
+void host_attention_forward(scalar_t *o, const scalar_t *q, const scalar_t *k, const scalar_t *v, int64_t BH,
+                            int64_t S, int64_t D, bool is_causal, scalar_t *out_m, scalar_t *out_l) {
+    const scalar_t neg_inf = -std::numeric_limits<scalar_t>::infinity();
+    const float scale = 1.0f / std::sqrt((float)D);
+    at::parallel_for(0, BH, 1, [&](int64_t begin, int64_t end) {
+        std::vector<scalar_t> row((size_t)S);
+        std::vector<scalar_t> acc((size_t)D);
+        for (int64_t b = begin; b < end; ++b) {
+            const scalar_t *qb = q + b * S * D;
+            const scalar_t *kb = k + b * S * D;
+            const scalar_t *vb = v + b * S * D;
+            scalar_t *ob = o + b * S * D;
+            for (int64_t i = 0; i < S; ++i) {
+                const scalar_t *qi = qb + i * D;
+                const int64_t visible = is_causal ? i + 1 : S;
+                for (int64_t j = 0; j < visible; ++j) {
+                    const scalar_t *kj = kb + j * D;
+                    scalar_t dot = 0;
+                    for (int64_t d = 0; d < D; ++d) dot += qi[d] * kj[d];
+                    row[j] = dot * scale;
+                }
+                for (int64_t j = visible; j < S; ++j) row[j] = neg_inf;
+                scalar_t mx = neg_inf;
+                for (int64_t j = 0; j < S; ++j) mx = std::max(row[j], mx);
+                double denom = 0;
+                for (int64_t j = 0; j < S; ++j) denom += std::exp((double)row[j] - mx);
+                out_m[b * S + i] = mx;
+                out_l[b * S + i] = denom;
+                for (int64_t d = 0; d < D; ++d) acc[d] = 0;
+                for (int64_t j = 0; j < S; ++j) {
+                    const scalar_t pj = std::exp(row[j] - mx) / denom;
+                    const scalar_t *vj = vb + j * D;
+                    for (int64_t d = 0; d < D; ++d) acc[d] += pj * vj[d];
+                }
+                for (int64_t d = 0; d < D; ++d) ob[i * D + d] = acc[d];
+            }
+        }
+    });
+}
+
+int32_t to_pmkl_dtype(at::ScalarType t) {
+    switch (t) {
+        case at::kFloat: return PMKL_DTYPE_F32;
+        case at::kHalf: return PMKL_DTYPE_F16;
+        case at::kBFloat16: return PMKL_DTYPE_BF16;
+        default: return -1;
+    }
+}
+
+// A device tensor the kernels can read in place: head_dim contiguous, 16-byte
+// aligned base and strides.  Anything else is copied contiguous first, as the
+// reference does with .contiguous() (fused_self_attention.cpp:160-162).
+at::Tensor device_view(const at::Tensor &t) {
+    const int64_t vec = 16 / t.element_size();
+    const bool ok = t.stride(3) == 1 && t.stride(0) % vec == 0 && t.stride(1) % vec == 0 && t.stride(2) % vec == 0 &&
+                    t.stride(2) >= t.size(3) && (reinterpret_cast<uintptr_t>(t.data_ptr()) % 16) == 0;
+    return ok ? t : t.contiguous();
+}
+
+void fill_strides(int64_t dst[3], const at::Tensor &t) {
+    dst[0] = t.stride(0);
+    dst[1] = t.stride(1);
+    dst[2] = t.stride(2);
+}
+
+}  // namespace
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_fw(const at::Tensor &q, const at::Tensor &k,
+                                                                       const at::Tensor &v, bool is_causal) {
+    TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "Input tensor shapes must match");
+    TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(), "Input tensor shapes must match");
+    TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
+                "Input tensor dtypes must match");
+    TORCH_CHECK(q.device() == k.device() && q.device() == v.device(), "Input tensors must be on one device");
+
+    const int64_t B = q.size(0), H = q.size(1), S = q.size(2), D = q.size(3);
+    auto opts = v.options().memory_format(at::MemoryFormat::Contiguous);
+    auto out = at::empty({B, H, S, D}, opts);
+    auto out_m = at::empty({B, H, S}, opts);
+    auto out_l = at::empty({B, H, S}, opts);
+
+    if (q.is_cpu()) {
+        AT_DISPATCH_FLOATING_TYPES_AND2(at::ScalarType::Half, at::ScalarType::BFloat16, v.scalar_type(),
+                                        "fused_self_attention_fw", [&]() {
+                                            auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
+                                            host_attention_forward<scalar_t>(
+                                                out.data_ptr<scalar_t>(), qc.data_ptr<scalar_t>(),
+                                                kc.data_ptr<scalar_t>(), vc.data_ptr<scalar_t>(), B * H, S, D,
+                                                is_causal, out_m.data_ptr<scalar_t>(), out_l.data_ptr<scalar_t>());
+                                        });
+        return std::forward_as_tuple(out, out_m, out_l);
+    }
+
+    TORCH_CHECK(q.is_cuda(), "fused_self_attention_fw: tensors must be on the CPU or a ROCm device, got ",
+                q.device());
+    const int32_t dt = to_pmkl_dtype(q.scalar_type());
+    TORCH_CHECK(dt >= 0, "fused_self_attention_fw: device path supports float32, float16 and bfloat16, got ",
+                q.scalar_type());
+    TORCH_CHECK(pmkl_attn_fwd_supported(dt, D), "fused_self_attention_fw: head_dim ", D,
+                " is not supported on the device (supported: 32, 64, 128)");
+    if (B * H * S == 0) return std::forward_as_tuple(out, out_m, out_l);
+
+    c10::OptionalDeviceGuard guard(q.device());
+    auto qd = device_view(q), kd = device_view(k), vd = device_view(v);
+    pmkl_attn_fwd_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = qd.data_ptr();
+    a.k = kd.data_ptr();
+    a.v = vd.data_ptr();
+    a.o = out.data_ptr();
+    a.m = out_m.data_ptr();
+    a.l = out_l.data_ptr();
+    a.dtype = dt;
+    a.ml_dtype = dt;
+    a.batch = B;
+    a.heads = H;
+    a.seq_len = S;
+    a.head_dim = D;
+    fill_strides(a.q_strides, qd);
+    fill_strides(a.k_strides, kd);
+    fill_strides(a.v_strides, vd);
+    fill_strides(a.o_strides, out);
+    a.scale = 0.f;
+    a.is_causal = is_causal ? 1 : 0;
+    hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+    const int rc = pmkl_attn_fwd(&a, (void *)stream);
+    TORCH_CHECK(rc == PMKL_OK, "fused_self_attention_fw: ", pmkl_last_error());
+    return std::forward_as_tuple(out, out_m, out_l);
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("fused_self_attention_fw", &fused_self_attention_fw, "fused_self_attention_fw",
+          pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("is_causal"));
+}
