@@ -1,0 +1,206 @@
+"""Benchmark of the fused causal self-attention forward on one MI355X.
+
+A step is one forward call (pmkl_attn_fwd through the C ABI) over one batch of
+the workload, inputs already resident in HBM.  Default workload: C3, bf16
+B=4 H=32 S=4096 D=128, causal, scale 1/sqrt(D) - the configuration the
+headline metric is quoted on.  Prints one JSON line.
+
+  value      whole-job TFLOP/s = causal FLOPs per step * steps / elapsed,
+             FLOPs = 2*B*H*D*S*(S+1) (QK^T and PV multiply-adds of the visible
+             pairs; softmax not counted)
+  roofline   the attention kernel against the dense bf16 MFMA peak
+             (2,516.6 TFLOP/s): achieved = FLOPs per launch / average launch
+             duration from HIP events on the launch stream; traffic = HBM bytes
+             per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
+             + WRITE_SIZE, scaled by a copy-kernel calibration), or null
+  cpu_baseline  the reference's own CPU operator (oracle/_ref, compiled from
+             pmkl_pytorch_ext/fused_self_attention.cpp) on a bounded sample:
+             one head of the same workload, timed single-threaded as written
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}   # dense MFMA, MI355X public spec
+PEAK_HBM_GBS = 8000.0
+METRIC = "causal-attn TFLOP/s on 1 MI355X, bf16 B4 H32 S4096 D128; % of MFMA peak"
+KERNEL_NAME = "attn_fwd_mfma16_kernel"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 512 MiB device copy (torch copy kernel) so that rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
+    return ap.parse_args()
+
+
+def calibrate_copy():
+    """One device-to-device copy of 512 MiB: reads 512 MiB, writes 512 MiB."""
+    import torch
+
+    n = 512 * 1024 * 1024 // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}))
+
+
+def read_traffic(config: str):
+    """HBM bytes per launch from profiles/pmc_<kernel>_<config>.txt, or None."""
+    path = ROOT / "profiles" / f"pmc_attn_fwd_{config}.txt"
+    if not path.exists():
+        return None
+    txt = path.read_text()
+    m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w):
+    """Reference CPU operator on one head of the workload (bounded sample)."""
+    import torch
+
+    from oracle import oracle
+    from pmkl_amd.workloads import host_inputs, torch_dtype
+
+    ref = oracle.reference_op()
+    if ref is None:
+        return None
+    q, k, v = host_inputs(w)
+    dt = torch_dtype(w.dtype)
+    sample = [torch.from_numpy(a[:1, :1].copy()).to(dt) for a in (q, k, v)]
+    torch.set_num_threads(1)
+    t0 = time.perf_counter()
+    ref.fused_self_attention_fw(sample[0], sample[1], sample[2], True)
+    dt_s = time.perf_counter() - t0
+    flops = oracle.causal_flops(1, 1, w.S, w.D)
+    return {
+        "value": flops / dt_s / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "reference",
+        "sample": f"1 of {w.B * w.H} heads of {w.name} (S={w.S}, D={w.D}, {w.dtype}, causal) through the "
+                  f"reference fused_self_attention_fw CPU body, single-threaded as written; {dt_s:.1f} s",
+        "seconds": dt_s,
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the attention path has no multi-GPU leg); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
+
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd.workloads import WORKLOADS, torch_inputs
+
+    w = WORKLOADS[args.config]
+    dev = torch.device("cuda:0")
+    q, k, v = torch_inputs(w, dev)
+    o = torch.empty_like(q)
+    m = torch.empty((w.B, w.H, w.S), dtype=q.dtype, device=dev)
+    l = torch.empty_like(m)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        pmkl_amd.attn_fwd(q, k, v, is_causal=True, out=o, out_m=m, out_l=l, stream=stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps bracketed by device syncs; events on the launch stream
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+
+    # per-launch durations (events around each launch) for the roofline figure
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in evs:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in evs)
+    avg_launch_ms = sum(per) / len(per)
+
+    from oracle.oracle import causal_flops
+
+    flops = causal_flops(w.B, w.H, w.S, w.D)
+    esize = {"bf16": 2, "fp16": 2, "fp32": 4}[w.dtype]
+    alg_bytes = (4 * w.B * w.H * w.S * w.D + 2 * w.B * w.H * w.S) * esize
+    elapsed_s = max(gpu_ms / 1e3, 1e-12)
+    value = flops * args.steps / elapsed_s / 1e12
+    achieved = flops / (avg_launch_ms / 1e3) / 1e12
+    peak = PEAK_TFLOPS[w.dtype]
+    traffic = read_traffic(w.name)
+
+    cpu = None if args.no_cpu else cpu_baseline(w)
+    if cpu is not None:
+        cpu.pop("seconds", None)
+
+    line = {
+        "metric": METRIC if w.name == "C3" else f"causal-attn TFLOP/s on 1 MI355X, {w.dtype} B{w.B} H{w.H} S{w.S} D{w.D}",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic: seeded PCG64 " + w.note,
+        "config": {"workload": f"{w.name} causal self-attention fwd {w.dtype} B{w.B} H{w.H} S{w.S} D{w.D}",
+                   "B": w.B, "H": w.H, "S": w.S, "D": w.D, "causal": True, "seed": w.seed,
+                   "flops_per_step": flops, "flop_count": "2*B*H*D*S*(S+1)",
+                   "alg_bytes_per_step": alg_bytes, "parallelism": "single GPU"},
+        "pct_of_mfma_peak": round(100.0 * value / peak, 2),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "kernel": KERNEL_NAME if w.dtype != "fp32" else "attn_fwd_f32_kernel",
+                     "avg_launch_us": round(avg_launch_ms * 1e3, 2), "min_launch_us": round(per[0] * 1e3, 2),
+                     "median_launch_us": round(per[len(per) // 2] * 1e3, 2),
+                     "hbm_GBs_algorithmic": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9, 1)},
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 4),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -13,10 +13,12 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/pmkl_attn.h"
 #include "attn_fwd_kernels.hpp"
+#include "attn_fwd_pipe.hpp"
 
 namespace {
 
@@ -50,18 +52,51 @@ bool head_dim_supported(int64_t d) { return d == 32 || d == 64 || d == 128; }
 using pmkl_amd::AttnParams;
 typedef void (*kernel_fn)(AttnParams);
 
-template <typename T, int D>
-kernel_fn pick16(bool causal) {
-    return causal ? (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, true>
-                  : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false>;
-}
-template <int D>
-kernel_fn pick32(bool causal) {
-    return causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, true>
-                  : (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, false>;
+// A kernel and its launch shape: threads per workgroup and query rows per workgroup.
+struct KernelChoice {
+    kernel_fn fn;
+    int threads;
+    int block_m;
+};
+
+int waves16() {
+    static const int w = [] {
+        const char *e = getenv("PMKL_ATTN_WAVES");
+        return (e && atoi(e) == 4) ? 4 : 8;
+    }();
+    return w;
 }
 
-kernel_fn select_kernel(int32_t dt, int64_t d, bool causal) {
+template <typename T, int D, int NW>
+KernelChoice pick16w(bool causal) {
+    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, true, NW>
+                   : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW>,
+            NW * 64, NW * 32};
+}
+bool use_pipe() {
+    static const bool v = [] {
+        const char *e = getenv("PMKL_ATTN_PIPE");
+        return e && atoi(e) == 1;
+    }();
+    return v;
+}
+
+template <typename T, int D>
+KernelChoice pick16(bool causal) {
+    if (use_pipe())
+        return {causal ? (kernel_fn)pmkl_amd::attn_fwd_pipe_kernel<T, D, true, 8>
+                       : (kernel_fn)pmkl_amd::attn_fwd_pipe_kernel<T, D, false, 8>,
+                512, 256};
+    return waves16() == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
+}
+template <int D>
+KernelChoice pick32(bool causal) {
+    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, true>
+                   : (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, false>,
+            pmkl_amd::kThreads, pmkl_amd::kBlockM};
+}
+
+KernelChoice select_kernel(int32_t dt, int64_t d, bool causal) {
     switch (dt) {
         case PMKL_DTYPE_BF16:
             if (d == 32) return pick16<__bf16, 32>(causal);
@@ -81,7 +116,7 @@ kernel_fn select_kernel(int32_t dt, int64_t d, bool causal) {
         default:
             break;
     }
-    return nullptr;
+    return {nullptr, 0, 0};
 }
 
 // Fills the three strides with the contiguous [B, H, S, D] ones when all are zero.
@@ -108,6 +143,9 @@ int check_tensor(const char *name, const void *ptr, const int64_t st[3], int64_t
     PMKL_REQUIRE(st[0] % vec == 0 && st[1] % vec == 0 && st[2] % vec == 0, PMKL_EINVAL,
                  "%s strides (%lld, %lld, %lld) must be multiples of %zu elements (16 bytes)", name,
                  (long long)st[0], (long long)st[1], (long long)st[2], vec);
+    // A 64-key tile is addressed by one 32-bit buffer range (bytes).
+    PMKL_REQUIRE(st[2] * (int64_t)esize * 64 < (1LL << 31), PMKL_EINVAL,
+                 "%s seq stride %lld is too large (a 64-row tile must span < 2 GiB)", name, (long long)st[2]);
     // The largest element offset must stay addressable with 64-bit arithmetic.
     const double span = (double)(B - 1) * st[0] + (double)(H - 1) * st[1] + (double)(S - 1) * st[2] + D;
     PMKL_REQUIRE(span < 9.0e18, PMKL_EINVAL, "%s spans too many elements", name);
@@ -144,7 +182,10 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
     PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
                  (long long)(B * H), (long long)S);
-    const int64_t n_qtiles = (S + pmkl_amd::kBlockM - 1) / pmkl_amd::kBlockM;
+    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0);
+    PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
+                 (long long)D);
+    const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;
     PMKL_REQUIRE(n_qtiles * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
                  (long long)(n_qtiles * B * H));
 
@@ -163,10 +204,6 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     const size_t ml_es = dtype_size(a->ml_dtype);
     PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
                  "m / l must be aligned to their element size");
-
-    kernel_fn fn = select_kernel(a->dtype, D, a->is_causal != 0);
-    PMKL_REQUIRE(fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
-                 (long long)D);
 
     AttnParams p;
     p.q = a->q;
@@ -187,9 +224,11 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
     p.scale_log2 = p.scale * 1.4426950408889634f;
     p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
+    // XCD-grouped issue order needs whole head pairs (causal) or heads per XCD.
+    p.xcd_order = (a->dtype != PMKL_DTYPE_F32 && getenv("PMKL_ATTN_NOXCD") == nullptr && (B * H) % (a->is_causal ? 16 : 8) == 0) ? 1 : 0;
 
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(fn, dim3((unsigned)(n_qtiles * B * H)), dim3(pmkl_amd::kThreads), 0, st, p);
+    hipLaunchKernelGGL(kc.fn, dim3((unsigned)(n_qtiles * B * H)), dim3(kc.threads), 0, st, p);
     hipError_t err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "kernel launch failed: %s", hipGetErrorString(err));
     return PMKL_OK;

@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace pmkl_amd {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -59,9 +61,10 @@ struct AttnParams {
     float scale;         // multiplies raw dot products
     float scale_log2;    // scale * log2(e)
     int32_t ml_f32;      // 1: m/l stored as float, 0: stored in the tensor dtype
+    int32_t xcd_order;   // 1: workgroups are issued XCD by XCD in head groups (pipelined kernel)
 };
 
-constexpr int kWaves = 4;                // waves per workgroup
+constexpr int kWaves = 4;                // waves per workgroup of the fp32 kernel
 constexpr int kThreads = kWaves * 64;    // 256
 constexpr int kBlockM = 32 * kWaves;     // query rows per workgroup (32 per wave)
 
@@ -102,6 +105,11 @@ template <> struct Elt16<__bf16> {
         bf16x2_t v = {(__bf16)a, (__bf16)b};
         return __builtin_bit_cast(uint32_t, v);
     }
+    // acc + lo + hi of a packed pair (v_dot2_f32_bf16 against {1, 1}).
+    static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+        const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, packed), one, acc, false);
+    }
 };
 template <> struct Elt16<_Float16> {
     typedef f16x8_t frag;
@@ -111,6 +119,10 @@ template <> struct Elt16<_Float16> {
     static __device__ __forceinline__ uint32_t pack2(float a, float b) {
         f16x2_t v = {(_Float16)a, (_Float16)b};
         return __builtin_bit_cast(uint32_t, v);
+    }
+    static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+        const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, packed), one, acc, false);
     }
 };
 
@@ -136,20 +148,49 @@ template <int CPR> __device__ __forceinline__ int swz_v(int row) {
     }
 }
 
+// Workgroup -> (head bh, query tile qt).  Default: blockIdx.x walks all heads
+// of one query tile at a time, longest tiles first when causal.  With
+// p.xcd_order (host sets it when B*H allows), blockIdx.x is read the way the
+// dispatcher places workgroups, round-robin over the 8 XCDs (XCD = L % 8):
+// each XCD walks its heads in pairs, longest query tile first within the pair
+// (causal), or one head at a time (non-causal).  An XCD's L2 then holds the K/V
+// of about two heads at a time while the longest tiles still start first.
+template <bool CAUSAL>
+__device__ __forceinline__ void map_workgroup(const AttnParams &p, int &bh, int &qt) {
+    const int L = blockIdx.x;
+    const int NQT = p.n_qtiles;
+    if (p.xcd_order) {
+        const int xcd = L & 7, k = L >> 3;
+        if (CAUSAL) {
+            const int grp = k / (2 * NQT), pos = k - grp * 2 * NQT;
+            qt = NQT - 1 - (pos >> 1);
+            bh = xcd + 8 * (2 * grp + (pos & 1));
+        } else {
+            bh = xcd + 8 * (k / NQT);
+            qt = k % NQT;
+        }
+    } else {
+        bh = L % p.BH;
+        qt = CAUSAL ? (NQT - 1 - L / p.BH) : (L / p.BH);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // 16-bit kernel (bf16 / fp16), head_dim D in {32, 64, 128}
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams p) {
+template <typename T, int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnParams p) {
     using E = Elt16<T>;
     using frag = typename E::frag;
+    constexpr int kThreads = NW * 64;
+    constexpr int kBlockM = 32 * NW;        // query rows per workgroup (32 per wave)
     constexpr int BN = 64;                  // keys per tile
     constexpr int CPR = D / 8;              // 16-byte chunks per row
     constexpr int TILE_CHUNKS = BN * CPR;   // chunks per K (or V) tile
-    constexpr int LOADS = TILE_CHUNKS / kThreads;
+    constexpr int LOADS = (TILE_CHUNKS + kThreads - 1) / kThreads;
+    constexpr bool PARTIAL = TILE_CHUNKS % kThreads != 0;   // some threads idle in the last load
     constexpr int NDB = D / 32;             // 32-wide blocks of head_dim
     constexpr int NDK = D / 16;             // 16-deep MFMA steps over head_dim
-    static_assert(TILE_CHUNKS % kThreads == 0, "tile not divisible by threads");
 
     __shared__ __attribute__((aligned(16))) T smem[2][2][BN * D];  // [stage][K,V]
 
@@ -162,9 +203,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
     // Longest-first order: blockIdx.x walks all heads of the last query tile
     // first.  Consecutive blocks of one head are BH apart, which keeps one
     // head on one XCD when BH is a multiple of 8.
-    const int L = blockIdx.x;
-    const int bh = L % p.BH;
-    const int qt = CAUSAL ? (p.n_qtiles - 1 - L / p.BH) : (L / p.BH);
+    int bh, qt;
+    map_workgroup<CAUSAL>(p, bh, qt);
     const int b = bh / p.H;
     const int h = bh - b * p.H;
     const int S = p.S;
@@ -191,28 +231,51 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
             qf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(src + 16 * dk));
     }
 
-    // Global -> register staging of one K/V tile.  Thread tid owns physical
-    // chunk slots j*256 + tid; it fetches the logical chunk that the swizzle
-    // places there.  Rows past the end of the sequence re-read row S-1 (finite
-    // data; those keys are masked).
-    u32x4_t kreg[LOADS], vreg[LOADS];
-    auto gload = [&](int kt) {
+    // Global -> register staging of one K/V tile with buffer loads.  Thread
+    // tid owns physical chunk slots j*256 + tid and fetches the logical chunk
+    // that the swizzle places there.  The buffer resource of each tile starts
+    // at its first key and ends at the last key of the sequence, so rows past
+    // the end read as zero (those keys are masked) and the per-thread byte
+    // offsets are the same for every tile.
+    // Two register sets: the loads of tile t go to set t & 1 two tiles ahead
+    // of use, so a load has two steps to land before its LDS write.
+    u32x4_t kreg[2][LOADS], vreg[2][LOADS];
+    int koff[LOADS], voff[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int sl = j * kThreads + tid;
+        const int row = sl / CPR;
+        const int pc = sl % CPR;
+        koff[j] = (int)((row * p.k_ss + 8 * (pc ^ swz_k<CPR>(row))) * (int64_t)sizeof(T));
+        voff[j] = (int)((row * p.v_ss + 8 * (pc ^ swz_v<CPR>(row))) * (int64_t)sizeof(T));
+    }
+    auto gload = [&](int kt, auto set_c) {
+        constexpr int SET = decltype(set_c)::value;
+        const int kbase = kt * BN;
+        const int rows = min(BN, S - kbase);
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(kg + (int64_t)kbase * p.k_ss), (short)0, (int)(((rows - 1) * p.k_ss + D) * sizeof(T)),
+            0x00020000);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(vg + (int64_t)kbase * p.v_ss), (short)0, (int)(((rows - 1) * p.v_ss + D) * sizeof(T)),
+            0x00020000);
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) {
-            const int sl = j * kThreads + tid;
-            const int row = sl / CPR;
-            const int pc = sl % CPR;
-            const int key = min(kt * BN + row, S - 1);
-            kreg[j] = *(const u32x4_t *)(kg + (int64_t)key * p.k_ss + 8 * (pc ^ swz_k<CPR>(row)));
-            vreg[j] = *(const u32x4_t *)(vg + (int64_t)key * p.v_ss + 8 * (pc ^ swz_v<CPR>(row)));
+            if (!PARTIAL || j * kThreads + tid < TILE_CHUNKS) {
+                kreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[j], 0, 0));
+                vreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[j], 0, 0));
+            }
         }
     };
-    auto swrite = [&](int st) {
+    auto swrite = [&](int st, auto set_c) {
+        constexpr int SET = decltype(set_c)::value;
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) {
             const int sl = j * kThreads + tid;
-            *(u32x4_t *)(&smem[st][0][sl * 8]) = kreg[j];
-            *(u32x4_t *)(&smem[st][1][sl * 8]) = vreg[j];
+            if (!PARTIAL || sl < TILE_CHUNKS) {
+                *(u32x4_t *)(&smem[st][0][sl * 8]) = kreg[SET][j];
+                *(u32x4_t *)(&smem[st][1][sl * 8]) = vreg[SET][j];
+            }
         }
     };
 
@@ -230,19 +293,32 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
     const int vrow0 = 16 * (g >> 1) + (tt >> 2);
     const int vcol0 = 16 * (g & 1) + 4 * (tt & 3);
 
-    gload(0);
-    swrite(0);
+    gload(0, std::integral_constant<int, 0>{});
+    swrite(0, std::integral_constant<int, 0>{});
+    // Q fragments and tile 0 have landed before the loop, so no vmcnt wait is
+    // needed before the score MFMAs of a tile; tile 1 is left in flight.
+    __builtin_amdgcn_s_waitcnt(0);
+    gload(min(1, nt - 1), std::integral_constant<int, 1>{});
     __syncthreads();
 
-    for (int kt = 0; kt < nt; ++kt) {
-        const int st = kt & 1;
-        if (kt + 1 < nt) gload(kt + 1);
+    // Tile kt: LDS stage kt & 1; its registers (set kt & 1) are refilled with
+    // tile kt + 2, and tile kt + 1 (set (kt+1) & 1) goes to the other stage.
+    auto tile_step = [&](auto set_c, int kt) {
+        constexpr int SET = decltype(set_c)::value;
+        constexpr int st = SET;
+        // Issued on every step (a clamped tile near the end) so that the
+        // number of loads in flight, and hence the vmcnt wait before the LDS
+        // write below, is the same on every path.
+        gload(min(kt + 2, nt - 1), set_c);
         const int kbase = kt * BN;
         const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
         if (wave_needed) {
             const T *Ks = smem[st][0];
             const T *Vs = smem[st][1];
             // ---- S^T = K Q^T for two 32-key blocks ----
+#ifdef PMKL_EXP_SETPRIO
+            __builtin_amdgcn_s_setprio(2);
+#endif
             f32x16_t sacc[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -258,6 +334,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
                     sacc[kb] = E::mma(a, qf[dk], sacc[kb]);
                 }
             }
+#ifdef PMKL_EXP_SETPRIO
+            __builtin_amdgcn_s_setprio(0);
+#endif
             // ---- mask (only tiles that straddle the diagonal or the end) ----
             const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
             if (need_mask) {
@@ -277,16 +356,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
             mx = half_max(mx);
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float alpha = fast_exp2((m_run - m_use) * p.scale_log2);
-            m_run = m_new;
-            l_run *= alpha;
+            // Rescale O and l only when some row max of this wave grew (a
+            // wave-uniform branch); the offset is always the exact running max.
+#ifdef PMKL_EXP_LAZY
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + PMKL_EXP_LAZY / p.scale_log2)) {
+#else
+            if (__builtin_amdgcn_ballot_w64(mx > m_run)) {
+#endif
+                const float m_new = fmaxf(m_run, mx);
+                const float alpha = fast_exp2((m_run - m_new) * p.scale_log2);  // 0 on the first tile
+                m_run = m_new;
+                l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < NDB; ++db)
+                for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-            const float moff = -m_use * p.scale_log2;
+                    for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+            }
+            const float moff = (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
             uint32_t pk[2][8];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -294,10 +380,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
                 for (int r = 0; r < 16; r += 2) {
                     const float p0 = fast_exp2(__builtin_fmaf(sacc[kb][r], p.scale_log2, moff));
                     const float p1 = fast_exp2(__builtin_fmaf(sacc[kb][r + 1], p.scale_log2, moff));
-                    l_run += p0 + p1;
                     pk[kb][r >> 1] = E::pack2(p0, p1);
+                    // l sums the probabilities as rounded for the PV product, so
+                    // O is normalised by exactly the weights it was built from.
+                    l_run = E::sum2(pk[kb][r >> 1], l_run);
                 }
             // ---- O^T += V^T P^T ----
+#ifdef PMKL_EXP_SETPRIO
+            __builtin_amdgcn_s_setprio(2);
+#endif
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -320,8 +411,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_mfma16_kernel(AttnParams
                     }
                 }
         }
-        if (kt + 1 < nt) swrite(st ^ 1);
+#ifdef PMKL_EXP_SETPRIO
+        __builtin_amdgcn_s_setprio(0);
+#endif
+        if (kt + 1 < nt) swrite(st ^ 1, std::integral_constant<int, SET ^ 1>{});
         __syncthreads();
+    };
+    for (int kt = 0; kt < nt; kt += 2) {
+        tile_step(std::integral_constant<int, 0>{}, kt);
+        if (kt + 1 < nt) tile_step(std::integral_constant<int, 1>{}, kt + 1);
     }
 
     // ---- epilogue: normalise, store O, m, l ----
