@@ -67,6 +67,7 @@ struct AttnParams {
 constexpr int kWaves = 4;                // waves per workgroup of the fp32 kernel
 constexpr int kThreads = kWaves * 64;    // 256
 constexpr int kBlockM = 32 * kWaves;     // query rows per workgroup (32 per wave)
+constexpr float kLazyLog2 = 8.0f;        // rescale threshold of the 16-bit kernel (log2 units)
 
 // ---------------------------------------------------------------------------
 // small device helpers
@@ -284,8 +285,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-    float m_run = -INFINITY;   // running row max, raw dot-product units
-    float l_run = 0.f;         // per-lane partial row sum relative to m_run
+    // Row max bookkeeping in raw dot-product units.  m_true is the exact
+    // running max (the m output); m_use is the offset of the exponentials,
+    // moved up to the running max only when some row of the wave outgrows it
+    // by more than kLazyLog2 in log2 units, so O and l are rescaled on a few
+    // tiles instead of every tile with a new max.  Probabilities then stay
+    // below 2^kLazyLog2, which bf16 / fp16 and the fp32 accumulators hold
+    // with their usual relative precision.
+    float m_true = -INFINITY;
+    float m_use = -INFINITY;
+    float l_run = 0.f;         // per-lane partial row sum relative to m_use
+    const float lazy_raw = kLazyLog2 / p.scale_log2;
 
     // Per-lane constant parts of the LDS addresses.
     const int arow = key_of_arow(col);        // K tile row read by this lane (per 32-key block)
@@ -316,9 +326,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             const T *Ks = smem[st][0];
             const T *Vs = smem[st][1];
             // ---- S^T = K Q^T for two 32-key blocks ----
-#ifdef PMKL_EXP_SETPRIO
-            __builtin_amdgcn_s_setprio(2);
-#endif
             f32x16_t sacc[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -334,9 +341,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                     sacc[kb] = E::mma(a, qf[dk], sacc[kb]);
                 }
             }
-#ifdef PMKL_EXP_SETPRIO
-            __builtin_amdgcn_s_setprio(0);
-#endif
             // ---- mask (only tiles that straddle the diagonal or the end) ----
             const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
             if (need_mask) {
@@ -358,21 +362,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             mx = half_max(mx);
             // Rescale O and l only when some row max of this wave grew (a
             // wave-uniform branch); the offset is always the exact running max.
-#ifdef PMKL_EXP_LAZY
-            if (__builtin_amdgcn_ballot_w64(mx > m_run + PMKL_EXP_LAZY / p.scale_log2)) {
-#else
-            if (__builtin_amdgcn_ballot_w64(mx > m_run)) {
-#endif
-                const float m_new = fmaxf(m_run, mx);
-                const float alpha = fast_exp2((m_run - m_new) * p.scale_log2);  // 0 on the first tile
-                m_run = m_new;
+            m_true = fmaxf(m_true, mx);
+            if (__builtin_amdgcn_ballot_w64(mx > m_use + lazy_raw)) {
+                const float m_new = fmaxf(m_use, mx);
+                const float alpha = fast_exp2((m_use - m_new) * p.scale_log2);  // 0 on the first tile
+                m_use = m_new;
                 l_run *= alpha;
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
             }
-            const float moff = (m_run == -INFINITY) ? 0.f : -m_run * p.scale_log2;
+            const float moff = (m_use == -INFINITY) ? 0.f : -m_use * p.scale_log2;
             uint32_t pk[2][8];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
@@ -386,9 +387,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                     l_run = E::sum2(pk[kb][r >> 1], l_run);
                 }
             // ---- O^T += V^T P^T ----
-#ifdef PMKL_EXP_SETPRIO
-            __builtin_amdgcn_s_setprio(2);
-#endif
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -411,9 +409,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                     }
                 }
         }
-#ifdef PMKL_EXP_SETPRIO
-        __builtin_amdgcn_s_setprio(0);
-#endif
         if (kt + 1 < nt) swrite(st ^ 1, std::integral_constant<int, SET ^ 1>{});
         __syncthreads();
     };
@@ -423,9 +418,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     }
 
     // ---- epilogue: normalise, store O, m, l ----
-    const float l_tot = half_sum(l_run);
+    const float l_sum = half_sum(l_run);   // relative to m_use
     if (wave_active && qi < S) {
-        const float inv = 1.0f / l_tot;
+        const float inv = 1.0f / l_sum;
+        // l of the output is relative to the exact row max
+        const float l_tot = l_sum * fast_exp2((m_use - m_true) * p.scale_log2);
         T *orow = og + (int64_t)qi * p.o_ss;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
@@ -438,7 +435,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             }
         if (hi == 0) {
             const int64_t mi = (int64_t)bh * S + qi;
-            const float mval = m_run * p.scale;
+            const float mval = m_true * p.scale;
             if (p.ml_f32) {
                 ((float *)p.m)[mi] = mval;
                 ((float *)p.l)[mi] = l_tot;
