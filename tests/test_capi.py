@@ -1,0 +1,122 @@
+"""CPU tests of the C ABI (include/pmkl_attn.h, pmkl_amd/libpmkl_attn.so).
+
+No kernel is launched here: the library is loaded, every declared symbol is
+resolved, and the argument checks are driven into each of their error paths
+(all of which return before any HIP call).  The error text must carry the
+file:line of the failed check, like the reference's CHECK_FAIL
+(pmkl/core/utils/exception.h:153-161).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from pmkl_amd import capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "pmkl_attn.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pmkl_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_exported_set():
+    assert _declared_functions() == sorted(capi.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = capi.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} is declared in pmkl_attn.h but not exported"
+
+
+def test_abi_version_and_support_matrix():
+    lib = capi.load()
+    assert lib.pmkl_abi_version() == 1
+    for dt in (capi.PMKL_DTYPE_F32, capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
+        for d in (32, 64, 128):
+            assert lib.pmkl_attn_fwd_supported(dt, d) == 1
+        for d in (0, 16, 80, 96, 256):
+            assert lib.pmkl_attn_fwd_supported(dt, d) == 0
+    assert lib.pmkl_attn_fwd_supported(7, 64) == 0
+
+
+def _args(**kw):
+    base = dict(q=0x1000, k=0x2000, v=0x3000, o=0x4000, m=0x5000, l=0x6000, dtype=capi.PMKL_DTYPE_BF16,
+                batch=1, heads=2, seq_len=64, head_dim=64)
+    base.update(kw)
+    return capi.make_args(**base)
+
+
+def _expect(args, code, pattern):
+    rc = capi.attn_fwd_raw(args)
+    msg = capi.last_error()
+    assert rc == code, (rc, msg)
+    assert re.search(pattern, msg), msg
+    assert re.search(r"pmkl check failed at attn_capi\.hip:\d+", msg), msg
+
+
+def test_error_paths():
+    lib = capi.load()
+    assert lib.pmkl_attn_fwd(None, None) == capi.PMKL_EINVAL
+    _expect(_args(dtype=9), capi.PMKL_EUNSUPPORTED, "unsupported dtype")
+    _expect(_args(ml_dtype=capi.PMKL_DTYPE_F16), capi.PMKL_EINVAL, "ml_dtype")
+    _expect(_args(batch=-1), capi.PMKL_EINVAL, "negative shape")
+    _expect(_args(head_dim=80), capi.PMKL_EUNSUPPORTED, "head_dim 80")
+    _expect(_args(scale=float("nan")), capi.PMKL_EINVAL, "scale")
+    _expect(_args(q=0), capi.PMKL_EINVAL, "q is a null pointer")
+    _expect(_args(v=0x3002), capi.PMKL_EINVAL, "v must be 16-byte aligned")
+    _expect(_args(k_strides=(2 * 64 * 64, 64 * 64, 32)), capi.PMKL_EINVAL, "seq stride >= head_dim")
+    _expect(_args(q_strides=(2 * 64 * 64, 64 * 64, 68)), capi.PMKL_EINVAL, "multiples of 8 elements")
+    _expect(_args(o_strides=(1 << 40, 1 << 30, 1 << 28)), capi.PMKL_EINVAL, "too large")
+    _expect(_args(m=0), capi.PMKL_EINVAL, "m / l must not be null")
+    _expect(_args(dtype=capi.PMKL_DTYPE_F32, ml_dtype=capi.PMKL_DTYPE_F32, m=0x5002), capi.PMKL_EINVAL,
+            "aligned to their element size")
+
+
+def test_empty_problem_returns_ok_without_touching_pointers():
+    """An empty problem returns before any pointer is used (causal_attention.h:270)."""
+    lib = capi.load()
+    for kw in (dict(seq_len=0), dict(batch=0), dict(heads=0)):
+        a = _args(q=0, k=0, v=0, o=0, m=0, l=0, **kw)
+        assert capi.attn_fwd_raw(a) == capi.PMKL_OK
+    assert lib.pmkl_causal_attention_forward(capi.PMKL_DTYPE_F32, None, None, None, None, 0, 4, 128, 64,
+                                             None, None, None) == capi.PMKL_OK
+
+
+def test_flat_entry_point_validates_like_the_template():
+    lib = capi.load()
+    rc = lib.pmkl_causal_attention_forward(capi.PMKL_DTYPE_BF16, None, None, None, None, 1, 1, 64, 96,
+                                           None, None, None)
+    assert rc == capi.PMKL_EUNSUPPORTED and "head_dim 96" in capi.last_error()
+    rc = lib.pmkl_causal_attention_forward(capi.PMKL_DTYPE_BF16, None, None, None, None, 1, 1, 64, 64,
+                                           None, None, None)
+    assert rc == capi.PMKL_EINVAL and "null pointer" in capi.last_error()
+
+
+def test_args_struct_layout_matches_header(tmp_path):
+    """Field offsets and size of the ctypes mirror equal those of the C struct,
+    as a C compiler lays it out from include/pmkl_attn.h."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    fields = [f[0] for f in capi.AttnFwdArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("%s %zu\\n", "{f}", offsetof(pmkl_attn_fwd_args, {f}));\n' for f in fields)
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "pmkl_attn.h"\nint main(void) {\n'
+                   + body + '  printf("sizeof %zu\\n", sizeof(pmkl_attn_fwd_args));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                         check=True).stdout.splitlines())
+    for f in fields:
+        assert int(out[f]) == getattr(capi.AttnFwdArgs, f).offset, f
+    assert int(out["sizeof"]) == ctypes.sizeof(capi.AttnFwdArgs)
