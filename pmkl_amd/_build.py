@@ -3,7 +3,6 @@
 Products (all next to their sources, so they travel with the tree):
   pmkl_amd/libpmkl_attn.so                 gfx950 kernels + C ABI (hipcc)
   pmkl_amd/pmkl_pytorch_ext.<ext-suffix>   torch operator over the C ABI (g++)
-  tests/cpp/_bin/test_causal_attention     C++ drop-in test of the C++ header (hipcc)
 
 Every function compiles unconditionally; nothing is skipped because an output
 already exists.
@@ -33,8 +32,6 @@ HIP_FLAGS = [
 CAPI_LIB = PKG / "libpmkl_attn.so"
 EXT_NAME = "pmkl_pytorch_ext"
 EXT_LIB = PKG / (EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
-CPP_TEST_SRC = ROOT / "tests" / "cpp" / "test_causal_attention.cpp"
-CPP_TEST_BIN = ROOT / "tests" / "cpp" / "_bin" / "test_causal_attention"
 
 
 def _run(cmd: list[str], cwd: Path = ROOT) -> None:
@@ -77,18 +74,8 @@ def build_torch_ext() -> Path:
     return EXT_LIB
 
 
-def build_cpp_tests() -> Path:
-    CPP_TEST_BIN.parent.mkdir(parents=True, exist_ok=True)
-    oracle_dir = ROOT / "oracle"
-    _run([HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), str(CPP_TEST_SRC),
-          f"-L{PKG}", "-lpmkl_attn", f"-L{oracle_dir}", "-loracle",
-          "-Wl,-rpath,$ORIGIN/../../../pmkl_amd", "-Wl,-rpath,$ORIGIN/../../../oracle",
-          "-o", str(CPP_TEST_BIN)])
-    return CPP_TEST_BIN
-
-
 def build_all(verbose: bool = True) -> None:
-    for step in (build_capi, build_torch_ext, build_cpp_tests):
+    for step in (build_capi, build_torch_ext):
         out = step()
         if verbose:
             print(f"[pmkl_amd build] {step.__name__}: {out.relative_to(ROOT)}", flush=True)

@@ -18,7 +18,6 @@
 
 #include "../../include/pmkl_attn.h"
 #include "attn_fwd_kernels.hpp"
-#include "attn_fwd_pipe.hpp"
 
 namespace {
 
@@ -73,20 +72,8 @@ KernelChoice pick16w(bool causal) {
                    : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW>,
             NW * 64, NW * 32};
 }
-bool use_pipe() {
-    static const bool v = [] {
-        const char *e = getenv("PMKL_ATTN_PIPE");
-        return e && atoi(e) == 1;
-    }();
-    return v;
-}
-
 template <typename T, int D>
 KernelChoice pick16(bool causal) {
-    if (use_pipe())
-        return {causal ? (kernel_fn)pmkl_amd::attn_fwd_pipe_kernel<T, D, true, 8>
-                       : (kernel_fn)pmkl_amd::attn_fwd_pipe_kernel<T, D, false, 8>,
-                512, 256};
     return waves16() == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
 }
 template <int D>

@@ -61,7 +61,7 @@ struct AttnParams {
     float scale;         // multiplies raw dot products
     float scale_log2;    // scale * log2(e)
     int32_t ml_f32;      // 1: m/l stored as float, 0: stored in the tensor dtype
-    int32_t xcd_order;   // 1: workgroups are issued XCD by XCD in head groups (pipelined kernel)
+    int32_t xcd_order;   // 1: workgroup index read as (XCD, head group, q-tile), see map_workgroup
 };
 
 constexpr int kWaves = 4;                // waves per workgroup of the fp32 kernel

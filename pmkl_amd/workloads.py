@@ -39,6 +39,12 @@ WORKLOADS = {
 }
 
 
+def causal_flops(B: int, H: int, S: int, D: int) -> int:
+    """Multiply-add FLOPs of QK^T and PV over the visible (j <= i) pairs:
+    4*D per pair, S*(S+1)/2 pairs per head (softmax not counted)."""
+    return 2 * B * H * D * S * (S + 1)
+
+
 def torch_dtype(name: str):
     import torch
 

@@ -43,3 +43,12 @@ def test_small_inputs_dtype_and_seed():
     assert all(torch.equal(x, y) for x, y in zip(a, b))
     assert not torch.equal(a[0], c[0])
     assert a[0].dtype == torch.bfloat16
+
+
+def test_causal_flops_counts_visible_pairs():
+    from pmkl_amd.workloads import causal_flops
+
+    for S in (1, 2, 7, 64):
+        pairs = sum(1 for i in range(S) for j in range(S) if j <= i)
+        assert causal_flops(1, 1, S, 16) == 4 * 16 * pairs
+    assert causal_flops(4, 32, 4096, 128) == 549_890_031_616
