@@ -16,8 +16,9 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "../../include/pmkl_attn.h"
+#include "pmkl_attn.h"
 #include "attn_fwd_kernels.hpp"
+#include "attn_fwd_w64.hpp"
 
 namespace {
 
@@ -72,8 +73,20 @@ KernelChoice pick16w(bool causal) {
                    : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW>,
             NW * 64, NW * 32};
 }
+bool use_w64() {
+    static const bool v = [] {
+        const char *e = getenv("PMKL_ATTN_W64");
+        return e && atoi(e) == 1;
+    }();
+    return v;
+}
+
 template <typename T, int D>
-KernelChoice pick16(bool causal) {
+KernelChoice pick16(bool causal, bool w64) {
+    if (w64)
+        return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, true>
+                       : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false>,
+                256, 256};
     return waves16() == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
 }
 template <int D>
@@ -83,17 +96,17 @@ KernelChoice pick32(bool causal) {
             pmkl_amd::kThreads, pmkl_amd::kBlockM};
 }
 
-KernelChoice select_kernel(int32_t dt, int64_t d, bool causal) {
+KernelChoice select_kernel(int32_t dt, int64_t d, bool causal, bool w64) {
     switch (dt) {
         case PMKL_DTYPE_BF16:
-            if (d == 32) return pick16<__bf16, 32>(causal);
-            if (d == 64) return pick16<__bf16, 64>(causal);
-            if (d == 128) return pick16<__bf16, 128>(causal);
+            if (d == 32) return pick16<__bf16, 32>(causal, w64);
+            if (d == 64) return pick16<__bf16, 64>(causal, w64);
+            if (d == 128) return pick16<__bf16, 128>(causal, w64);
             break;
         case PMKL_DTYPE_F16:
-            if (d == 32) return pick16<_Float16, 32>(causal);
-            if (d == 64) return pick16<_Float16, 64>(causal);
-            if (d == 128) return pick16<_Float16, 128>(causal);
+            if (d == 32) return pick16<_Float16, 32>(causal, w64);
+            if (d == 64) return pick16<_Float16, 64>(causal, w64);
+            if (d == 128) return pick16<_Float16, 128>(causal, w64);
             break;
         case PMKL_DTYPE_F32:
             if (d == 32) return pick32<32>(causal);
@@ -169,13 +182,6 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
     PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
                  (long long)(B * H), (long long)S);
-    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0);
-    PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
-                 (long long)D);
-    const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;
-    PMKL_REQUIRE(n_qtiles * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
-                 (long long)(n_qtiles * B * H));
-
     const size_t es = dtype_size(a->dtype);
     int64_t qs[3], ks[3], vs[3], os[3];
     default_strides(qs, a->q_strides, H, S, D);
@@ -187,6 +193,19 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     if ((rc = check_tensor("k", a->k, ks, B, H, S, D, es)) != PMKL_OK) return rc;
     if ((rc = check_tensor("v", a->v, vs, B, H, S, D, es)) != PMKL_OK) return rc;
     if ((rc = check_tensor("o", a->o, os, B, H, S, D, es)) != PMKL_OK) return rc;
+
+    // The 64-row kernel addresses a head's whole K / V through one buffer
+    // resource with 32-bit offsets.
+    auto head_span_ok = [&](const int64_t *st) {
+        return st[2] >= 0 && ((S - 1) * st[2] + D) * (int64_t)es < (1LL << 31);
+    };
+    const bool w64 = use_w64() && a->dtype != PMKL_DTYPE_F32 && head_span_ok(ks) && head_span_ok(vs);
+    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64);
+    PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
+                 (long long)D);
+    const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;
+    PMKL_REQUIRE(n_qtiles * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
+                 (long long)(n_qtiles * B * H));
     PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
     const size_t ml_es = dtype_size(a->ml_dtype);
     PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,

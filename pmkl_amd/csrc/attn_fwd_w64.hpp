@@ -1,0 +1,566 @@
+// 64-rows-per-wave variant of the 16-bit attention kernel (gfx950).
+//
+// Same layouts and arithmetic as attn_fwd_mfma16_kernel (transposed scores
+// S^T = K Q^T, P kept in registers as the B operand of O^T = V^T P^T, V^T from
+// ds_read_b64_tr_b16, lazy rescale).  One wave per SIMD (4 waves, 256 query
+// rows per workgroup); each wave owns two 32-row blocks, and every K or V
+// fragment it reads from LDS feeds one MFMA of each block, which halves the
+// LDS operand reads per MFMA.
+//
+// Software pipeline: iteration t issues, one MFMA per slot,
+//   slots 0 .. QKS-1       QK of tile t+1 (both blocks, score set (t+1) & 1)
+//   slots QKS .. NSLOT-1   PV of tile t   (both blocks)
+// and behind every MFMA a share of the VALU work, placed at compile time
+// (W64Sched): the exponentials, packing and row sums of tile t, finished a
+// slot before the PV MFMA that reads them, then the row maxima of tile t+1
+// once its QK is done.  The wave issues in order, so what stands between two
+// MFMAs must fit under one MFMA (~32 clocks of the matrix core): an MFMA
+// issued straight behind another stalls the wave, and its VALU share with it.
+// sched_barrier fences pin every slot; asm-volatile register pins keep the
+// IR optimizer from sinking VALU work towards its consumers.
+//
+// Operands: K fragments of tile t+1 then V^T fragments of tile t form one
+// stream of NF fragments per iteration, read from LDS RING fragments ahead of
+// their MFMAs into a ring of registers (NF % RING == 0, so the ring position
+// of a fragment is the same in every iteration); the last RING reads of an
+// iteration already fetch the first K fragments of the next one.
+//
+// Registers: O^T accumulators (2 x D/32 x 16) and the Q fragments live in
+// AGPRs, used only by MFMAs issued from inline asm; scores, P and operands
+// live in VGPRs.  The compiler cannot see inside those MFMAs, so the kernel
+// keeps the MFMA -> VALU hazard distances itself (w64_mfma_drain before the
+// first VALU access of an MFMA result, and P written a full slot before the
+// MFMA that reads it).
+//
+// LDS: K/V tiles reach LDS by LDS-DMA (buffer_load ... lds) into three slots
+// each, K(t) and V(t) in slot t % 3.  Iteration t issues the DMAs of K(t+3)
+// and V(t+2); one barrier per iteration, BARS slots in, after the wave's last
+// LDS read of K(t+1) and V(t), preceded by a wait for the DMAs of iteration
+// t-1 (K(t+2), V(t+1)).  So a DMA only overwrites a slot all waves have
+// finished reading (K(t), V(t-1), read before the previous barrier), and a
+// tile is read only after the barrier that follows its arrival.
+#pragma once
+
+#include "attn_fwd_kernels.hpp"
+
+namespace pmkl_amd {
+
+// One LDS-DMA of 16 bytes per lane: bytes [off, off+16) of buffer r land at
+// LDS byte address m0 + 16 * lane.  Inline asm, so the compiler neither waits
+// for it before unrelated LDS reads nor counts it; the kernel waits itself.
+__device__ __forceinline__ void w64_lds_dma16(__amdgpu_buffer_rsrc_t r, int off, unsigned m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0), "s"(r)
+                 : "memory");
+}
+
+// MFMAs with operands pinned to register files:
+//   pv    c (AGPRs) += a * b
+//   qk0   d (VGPRs)  = a * b (b in AGPRs)
+//   qk    d (VGPRs) += a * b (b in AGPRs)
+template <typename T> struct W64Mma;
+template <> struct W64Mma<__bf16> {
+    static __device__ __forceinline__ void pv(f32x16_t &c, bf16x8_t a, bf16x8_t b) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
+    static __device__ __forceinline__ void qk0(f32x16_t &d, bf16x8_t a, bf16x8_t b) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b));
+    }
+    static __device__ __forceinline__ void qk(f32x16_t &d, bf16x8_t a, bf16x8_t b) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b));
+    }
+};
+template <> struct W64Mma<_Float16> {
+    static __device__ __forceinline__ void pv(f32x16_t &c, f16x8_t a, f16x8_t b) {
+        asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
+    static __device__ __forceinline__ void qk0(f32x16_t &d, f16x8_t a, f16x8_t b) {
+        asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b));
+    }
+    static __device__ __forceinline__ void qk(f32x16_t &d, f16x8_t a, f16x8_t b) {
+        asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b));
+    }
+};
+// 24 wait states: enough between an MFMA writing registers and VALU reading
+// or writing them, for every MFMA used here.
+__device__ __forceinline__ void w64_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
+// s = (R <= d) ? s : -inf, through VCC: left to itself the compiler computes
+// all compares of a tile into separate SGPR pairs first, and that pressure
+// spills long-lived SGPRs for the whole loop.
+template <int R>
+__device__ __forceinline__ float w64_mask_key(float s, int d) {
+    asm volatile("v_cmp_le_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %3, %0, vcc" : "+v"(s) : "n"(R), "v"(d), "v"(-INFINITY) : "vcc");
+    return s;
+}
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled at compile time.
+template <int B, int E, typename F>
+__device__ __forceinline__ void w64_static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        w64_static_for<B + 1, E>(f);
+    }
+}
+
+// Compile-time slot schedule of one iteration (head_dim D).
+template <int D> struct W64Sched {
+    static constexpr int NDB = D / 32;            // 32-wide blocks of head_dim
+    static constexpr int NDK = D / 16;            // 16-deep MFMA steps over head_dim
+    static constexpr int NKF = 2 * NDK;           // K fragments per tile: (dk, kb)
+    static constexpr int NVF = 4 * NDB;           // V^T fragments per tile: (kb, c, db)
+    static constexpr int NF = NKF + NVF;          // fragments per iteration
+    static constexpr int NSLOT = 2 * NF;          // MFMAs per iteration
+    static constexpr int QKS = 2 * NKF;           // first PV slot
+    static constexpr int RING = 4;                // fragments read ahead
+    static constexpr int BARS = NSLOT - 2 * RING + 1;   // barrier slot: before the first next-tile read
+    static_assert(NF % RING == 0, "ring position must repeat every iteration");
+
+    // Exponential pairs in the order the PV MFMAs read them: pair i covers
+    // score registers 2 r2 and 2 r2 + 1 of block qb, key block kb; the PV
+    // fragments (kb, c, *) read pairs 4c .. 4c+3 of (qb, kb).
+    static constexpr int pair_c(int i) { return (i >> 3) & 1; }
+    static constexpr int pair_kb(int i) { return i >> 4; }
+    static constexpr int pair_qb(int i) { return (i >> 2) & 1; }
+    static constexpr int pair_r2(int i) { return 4 * pair_c(i) + (i & 3); }
+    static constexpr int pair_need(int i) { return QKS + 2 * NDB * (2 * pair_kb(i) + pair_c(i)); }
+
+    // Exponential units, three per pair: A (first exp), B (second), C (pack
+    // and row sums), in the stream A0 B0 A1 B1 C0 A2 B2 C1 ... A31 B31 C30 C31,
+    // spread evenly over slots 0 .. ES-1.
+    static constexpr int NU = 96;
+    static constexpr int ES = QKS + 6 * NDB - 1;
+    static constexpr int unit_slot(int n) { return n * ES / NU; }
+    static constexpr int unit_first(int s) { return (s * NU + ES - 1) / ES; }   // first unit of slot s
+    static constexpr int unit_kind(int n) { return n < 2 ? n : n == NU - 1 ? 2 : (n - 2) % 3; }
+    static constexpr int unit_pair(int n) {
+        return n < 2 ? 0 : n == NU - 1 ? 31 : (n - 2) % 3 == 2 ? (n - 2) / 3 : (n - 2) / 3 + 1;
+    }
+    static constexpr int c_unit(int i) { return i == 31 ? NU - 1 : 3 * i + 4; }
+
+    // Maxima of tile t+1: drain and mask at slot MS0, then 8 partial maxima
+    // (qb, kb, half), the two block maxima and the two block updates.
+    static constexpr int NMU = 12;
+    static constexpr int MS0 = QKS + 2;
+    static constexpr int max_slot(int k) { return MS0 + k * (NSLOT - 1 - MS0) / (NMU - 1); }
+
+    // DMAs of the iteration, all before the barrier.
+    static constexpr int dma_slot(int j, int n) { return 1 + j * (BARS - 1) / n; }
+
+    static constexpr bool valid() {
+        for (int n = 0; n < NU; ++n)
+            if (unit_slot(n) < 0 || unit_slot(n) >= ES || unit_first(unit_slot(n)) > n ||
+                unit_first(unit_slot(n) + 1) <= n)
+                return false;
+        for (int i = 0; i < 32; ++i)
+            if (unit_slot(c_unit(i)) > pair_need(i) - 2) return false;   // P ready a slot early
+        // The block updates change the exponent offsets: after every exponential.
+        if (max_slot(10) < ES) return false;
+        if (max_slot(NMU - 1) != NSLOT - 1) return false;
+        return BARS > QKS && BARS % 2 == 1;
+    }
+    static_assert(valid(), "slot schedule");
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_fwd_w64_kernel(AttnParams p) {
+    using E = Elt16<T>;
+    using M = W64Mma<T>;
+    using Sch = W64Sched<D>;
+    using frag = typename E::frag;
+    constexpr int kBlockM = 256;            // query rows per workgroup (64 per wave)
+    constexpr int BN = 64;                  // keys per tile
+    constexpr int CPR = D / 8;              // 16-byte chunks per row
+    constexpr int TILE_CHUNKS = BN * CPR;   // chunks per K (or V) tile
+    constexpr int LOADS = TILE_CHUNKS / 256;   // DMAs per thread per tensor per tile
+    constexpr int TILE_BYTES = BN * D * (int)sizeof(T);
+    constexpr int NDB = Sch::NDB, NDK = Sch::NDK, NKF = Sch::NKF, NF = Sch::NF;
+    constexpr int NSLOT = Sch::NSLOT, RING = Sch::RING;
+    static_assert(TILE_CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
+
+    __shared__ __attribute__((aligned(1024))) T smem[6][BN * D];   // K slots 0-2, V slots 3-5
+    const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) T *)smem[0];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int col = lane & 31;
+
+    int bh, qt;
+    map_workgroup<CAUSAL>(p, bh, qt);
+    const int b = bh / p.H;
+    const int h = bh - b * p.H;
+    const int S = p.S;
+
+    const T *qg = (const T *)p.q + b * p.q_sb + h * p.q_sh;
+    const T *kg = (const T *)p.k + b * p.k_sb + h * p.k_sh;
+    const T *vg = (const T *)p.v + b * p.v_sb + h * p.v_sh;
+    T *og = (T *)p.o + b * p.o_sb + h * p.o_sh;
+
+    const int q0 = qt * kBlockM;
+    const int q0w = q0 + 64 * wave;                   // first row of the wave
+    const int last_key = CAUSAL ? min(q0 + kBlockM - 1, S - 1) : S - 1;
+    const int nt = last_key / BN + 1;                 // key tiles of the workgroup
+    const int nt2 = (nt + 1) & ~1;                    // iterations run by every wave
+    const bool wave_active = q0w < S;
+    // Tiles this wave computes: 0 .. ntw-1; only tile ntw-1 can hold keys past
+    // a row of the wave (causal diagonal) or past S.  Rounded up to even, the
+    // extra tile being fully masked.
+    const int ntw = !wave_active ? 0 : CAUSAL ? min(nt, (q0w + 63) / BN + 1) : nt;
+    const int ntw2 = (ntw + 1) & ~1;
+
+    // Q fragments (B operand of S^T = K Q^T, AGPRs): block qb, lane holds
+    // Q[q0w + 32 qb + col][16 dk + 8 hi .. +7].
+    frag qf[2][NDK];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int qrow = min(q0w + 32 * qb + col, S - 1);
+        const T *src = qg + (int64_t)qrow * p.q_ss + 8 * hi;
+#pragma unroll
+        for (int dk = 0; dk < NDK; ++dk)
+            qf[qb][dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(src + 16 * dk));
+    }
+
+    // ---- DMA staging: lane `lane` of wave `wave` fills chunk slot
+    // j*256 + 64*wave + lane, i.e. LDS bytes slot_base + 4096 j + 1024 wave
+    // + 16 lane, with the logical chunk the XOR swizzle places there.
+    int koff[LOADS], voff[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int sl = j * 256 + tid;
+        const int row = sl / CPR;
+        const int pc = sl % CPR;
+        koff[j] = (int)((row * p.k_ss + 8 * (pc ^ swz_k<CPR>(row))) * (int64_t)sizeof(T));
+        voff[j] = (int)((row * p.v_ss + 8 * (pc ^ swz_v<CPR>(row))) * (int64_t)sizeof(T));
+    }
+    // Buffer resources of the head's K and V, from key 0 to the last key of
+    // the sequence: rows past S read as zero (those keys are masked).  The
+    // host keeps (S - 1) * stride + D elements within 2^31 bytes.
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)kg, (short)0, (int)(((S - 1) * p.k_ss + D) * sizeof(T)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)vg, (short)0, (int)(((S - 1) * p.v_ss + D) * sizeof(T)), 0x00020000);
+    const int k_tile_bytes = (int)(BN * p.k_ss * sizeof(T));
+    const int v_tile_bytes = (int)(BN * p.v_ss * sizeof(T));
+    const unsigned lds_w = lds0 + (unsigned)(wave * 1024);
+    // DMA j of K / V tile kt (data clamped to the last tile) into LDS slot
+    // sl = kt % 3 (kept by the caller).
+    auto dma_k = [&](int kt, int sl, int j) __attribute__((always_inline)) {
+        w64_lds_dma16(krs, koff[j] + min(kt, nt - 1) * k_tile_bytes,
+                      lds_w + (unsigned)(sl * TILE_BYTES + j * 4096));
+    };
+    auto dma_v = [&](int kt, int sl, int j) __attribute__((always_inline)) {
+        w64_lds_dma16(vrs, voff[j] + min(kt, nt - 1) * v_tile_bytes,
+                      lds_w + (unsigned)((3 + sl) * TILE_BYTES + j * 4096));
+    };
+    // DMA i of iteration t: K(t+3) into slot t % 3 (sl0), then V(t+2) into
+    // slot (t+2) % 3 (sl2).
+    auto dma_step = [&](int t, int sl0, int sl2, int i) __attribute__((always_inline)) {
+        if (i < LOADS) dma_k(t + 3, sl0, i);
+        else dma_v(t + 2, sl2, i - LOADS);
+    };
+    // Wait until only the DMAs of the current iteration (2 * LOADS) may be in
+    // flight and the wave's LDS reads have returned, then barrier.
+    auto sync_tiles = [&]() __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(2 * LOADS) : "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    f32x16_t acc[2][NDB];      // O^T accumulators, AGPRs
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.f;
+    f32x16_t sc[2][2][2];      // [set][qb][kb] scores; tile t uses set t & 1
+    uint32_t pk[2][2][8];      // [qb][kb][pair] probabilities of the tile in PV
+    float pe[2][2];            // exponentials of a pair until packed, by pair parity
+    float m_true[2] = {-INFINITY, -INFINITY};
+    float m_use[2] = {-INFINITY, -INFINITY};
+    float moff[2] = {0.f, 0.f};   // -m_use * scale_log2 (0 while m_use is -inf)
+    float alpha[2] = {1.f, 1.f};
+    bool rescale[2] = {false, false};
+    float l_a[2] = {0.f, 0.f}, l_b[2] = {0.f, 0.f};   // two partial row sums per block
+    const float lazy_raw = kLazyLog2 / p.scale_log2;
+
+    const int arow = key_of_arow(col);
+    const int g16 = lane >> 4, tt = lane & 15;
+    const int vrow0 = 16 * (g16 >> 1) + (tt >> 2);
+    const int vcol0 = 16 * (g16 & 1) + 4 * (tt & 3);
+    const uint32_t krow_off = (uint32_t)(arow * D * sizeof(T));
+    const uint32_t kx16 = (uint32_t)((hi ^ swz_k<CPR>(arow)) * 16);
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    typedef __attribute__((address_space(3))) u32x4_t lds_u32x4;
+    typedef short s16x8_t __attribute__((ext_vector_type(8)));
+
+    // Lane part of the LDS byte address of K fragment (dk, *): row
+    // key_of_arow(col), 16-byte chunk 2 dk + hi through the swizzle.
+    uint32_t kaddr[NDK];
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) kaddr[dk] = krow_off + (((uint32_t)(32 * dk)) ^ kx16);
+    // K fragment f = (dk, kb) = (f >> 1, f & 1) of the tile in the LDS slot
+    // starting at byte kslot_b.
+    auto kfrag = [&](uint32_t kslot_b, int f) __attribute__((always_inline)) {
+        const int dk = f >> 1, kb = f & 1;
+        const uint32_t addr = kaddr[dk] + kslot_b + (uint32_t)(kb * 32 * D * sizeof(T));
+        return __builtin_bit_cast(frag, *(const lds_u32x4 *)(uintptr_t)addr);
+    };
+    // V^T fragment f = (kb, c, db): 32 head-dim columns x 16 keys.
+    auto vfrag = [&](const T *Vs, int f) __attribute__((always_inline)) {
+        const int kb = f / (2 * NDB), c = (f / NDB) % 2, db = f % NDB;
+        const int r0 = 32 * kb + 8 * c + vrow0;
+        const int cc = 32 * db + vcol0;
+        const int ch = cc >> 3, part = cc & 7;
+        const T *a0 = Vs + r0 * D + 8 * (ch ^ swz_v<CPR>(r0)) + part;
+        const T *a1 = Vs + (r0 + 4) * D + 8 * (ch ^ swz_v<CPR>(r0 + 4)) + part;
+        s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a0);
+        s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a1);
+        return __builtin_bit_cast(frag, s16x8_t{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]});
+    };
+    auto k_slot_base = [&](int sl) __attribute__((always_inline)) { return lds0 + (uint32_t)(sl * TILE_BYTES); };
+
+    // ---- softmax pieces ----
+    // Mask of tile kt (score set SET): tile ntw-1 against the diagonal / S,
+    // later tiles entirely (a fully masked tile changes nothing).
+    auto sm_mask = [&](int kt, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        if (kt >= ntw - 1) {
+            const int kbase = kt * BN;
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                const int qi = q0w + 32 * qb + col;
+                const int lim = kt == ntw - 1 ? (CAUSAL ? min(qi, S - 1) : S - 1) : -1;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    // register r holds key kbase + 32 kb + 16 hi + r: kept iff r <= d
+                    const int d = lim - (kbase + 32 * kb + 16 * hi);
+                    w64_static_for<0, 16>([&](auto r_c) __attribute__((always_inline)) {
+                        constexpr int r = decltype(r_c)::value;
+                        sc[SET][qb][kb][r] = w64_mask_key<r>(sc[SET][qb][kb][r], d);
+                    });
+                }
+            }
+        }
+    };
+    float mx[2], mh[2];
+    // Max unit k of score set SET: k < 8 partial row max (qb, kb, half);
+    // k = 8, 9 the row max of block k - 8 (both lane halves); k = 10, 11 the
+    // update of block k - 10: exact running max and the lazy rescale decision,
+    // without branches (the O rescale itself waits for the PV MFMAs in flight).
+    // Split so that no dependency chain stalls the in-order issue for long.
+    auto max_unit = [&](auto set_c, int k) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        if (k < 8) {
+            const int qb = k >> 2, kb = (k >> 1) & 1, r0 = 8 * (k & 1);
+            float m = (k & 3) == 0 ? sc[SET][qb][0][0] : mx[qb];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) m = fmaxf(m, sc[SET][qb][kb][r0 + r]);
+            asm volatile("" : "+v"(m));
+            mx[qb] = m;
+        } else if (k < 10) {
+            const int qb = k - 8;
+            mh[qb] = half_max(mx[qb]);
+            asm volatile("" : "+v"(mh[qb]));
+        } else {
+            const int qb = k - 10;
+            const float m = mh[qb];
+            m_true[qb] = fmaxf(m_true[qb], m);
+            const bool up = __builtin_amdgcn_ballot_w64(m > m_use[qb] + lazy_raw) != 0;
+            const float m_new = fmaxf(m_use[qb], m);
+            alpha[qb] = fast_exp2((m_use[qb] - m_new) * p.scale_log2);   // read only when up; 0 on the first tile
+            const float mo = m_new == -INFINITY ? 0.f : -m_new * p.scale_log2;
+            rescale[qb] = up;
+            m_use[qb] = up ? m_new : m_use[qb];
+            moff[qb] = up ? mo : moff[qb];
+        }
+    };
+    auto apply_rescale = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+            if (rescale[qb]) {
+                l_a[qb] *= alpha[qb];
+                l_b[qb] *= alpha[qb];
+                w64_mfma_drain();
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[qb][db][r] *= alpha[qb];
+                w64_mfma_drain();
+                rescale[qb] = false;
+            }
+    };
+    // Exponential unit n of score set SET (see W64Sched).  Every result is
+    // pinned where it is computed: without a use there, IR-level sinking
+    // moves the work next to the PV MFMAs that consume P, in one clump.
+    auto exp_unit = [&](auto set_c, auto n_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        constexpr int n = decltype(n_c)::value;
+        constexpr int kind = Sch::unit_kind(n), i = Sch::unit_pair(n);
+        constexpr int qb = Sch::pair_qb(i), kb = Sch::pair_kb(i), r = 2 * Sch::pair_r2(i);
+        if constexpr (kind < 2) {
+            pe[i & 1][kind] = fast_exp2(__builtin_fmaf(sc[SET][qb][kb][r + kind], p.scale_log2, moff[qb]));
+            asm volatile("" : "+v"(pe[i & 1][kind]));
+        } else {
+            pk[qb][kb][r >> 1] = E::pack2(pe[i & 1][0], pe[i & 1][1]);
+            l_a[qb] += pe[i & 1][0];
+            l_b[qb] += pe[i & 1][1];
+            asm volatile("" : "+v"(pk[qb][kb][r >> 1]), "+v"(l_a[qb]), "+v"(l_b[qb]));
+        }
+    };
+
+    frag ring[RING];
+    // Iteration t (tile scores in set SET = t & 1): QK of tile t+1 into set
+    // SET ^ 1 and PV of tile t, with the VALU work of the schedule.  LDS
+    // slots: sl0 = t % 3, sl1 = (t+1) % 3, sl2 = (t+2) % 3.
+    auto iteration = [&](int t, auto set_c, int sl0, int sl1, int sl2) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        using NSET = std::integral_constant<int, SET ^ 1>;
+        using CSET = std::integral_constant<int, SET>;
+        const uint32_t kcur = k_slot_base(sl1);
+        const uint32_t knext = k_slot_base(sl2);
+        const T *Vs = smem[3 + sl0];
+        w64_static_for<0, NSLOT>([&](auto s_c) __attribute__((always_inline)) {
+            constexpr int s = decltype(s_c)::value;
+            constexpr int g = s >> 1, qb = s & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (g < NKF) {
+                constexpr int dk = g >> 1, kb = g & 1;
+                if constexpr (dk == 0) M::qk0(sc[SET ^ 1][qb][kb], ring[g % RING], qf[qb][0]);
+                else M::qk(sc[SET ^ 1][qb][kb], ring[g % RING], qf[qb][dk]);
+            } else {
+                constexpr int f = g - NKF;
+                constexpr int kb = f / (2 * NDB), c = (f / NDB) % 2, db = f % NDB;
+                u32x4_t bw = {pk[qb][kb][4 * c], pk[qb][kb][4 * c + 1], pk[qb][kb][4 * c + 2], pk[qb][kb][4 * c + 3]};
+                M::pv(acc[qb][db], ring[g % RING], __builtin_bit_cast(frag, bw));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (s == Sch::BARS) sync_tiles();
+            if constexpr (qb == 1) {   // fragment g is done: refill its ring entry
+                constexpr int gn = g + RING;
+                if constexpr (gn < NKF) ring[g % RING] = kfrag(kcur, gn);
+                else if constexpr (gn < NF) ring[g % RING] = vfrag(Vs, gn - NKF);
+                else ring[g % RING] = kfrag(knext, gn - NF);
+            }
+            w64_static_for<0, 2 * LOADS>([&](auto j_c) __attribute__((always_inline)) {
+                constexpr int j = decltype(j_c)::value;
+                if constexpr (Sch::dma_slot(j, 2 * LOADS) == s) dma_step(t, sl0, sl2, j);
+            });
+            if constexpr (s == Sch::MS0) {
+                w64_mfma_drain();   // the QK MFMAs of tile t+1 have written the scores
+                sm_mask(t + 1, NSET{});
+            }
+            if constexpr (s < Sch::ES)
+                w64_static_for<Sch::unit_first(s), Sch::unit_first(s + 1)>(
+                    [&](auto n_c) __attribute__((always_inline)) { exp_unit(CSET{}, n_c); });
+            w64_static_for<0, Sch::NMU>([&](auto k_c) __attribute__((always_inline)) {
+                constexpr int k = decltype(k_c)::value;
+                if constexpr (Sch::max_slot(k) == s) max_unit(NSET{}, k);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        apply_rescale();   // decided for tile t+1; the PV MFMAs of tile t are issued
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+
+    // ---- prologue: K(0), V(0), K(1) landed; K(2), V(1) in flight ----
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        dma_k(0, 0, j);
+        dma_v(0, 0, j);
+    }
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) dma_k(1, 1, j);
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        dma_k(2, 2, j);
+        dma_v(1, 1, j);
+    }
+    sync_tiles();
+    // Scores and maxima of tile 0.
+    {
+        const uint32_t k0 = k_slot_base(0);
+#pragma unroll
+        for (int f = 0; f < NKF; ++f) {
+            const frag a = kfrag(k0, f);
+            const int dk = f >> 1, kb = f & 1;
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                if (dk == 0) M::qk0(sc[0][qb][kb], a, qf[qb][0]);
+                else M::qk(sc[0][qb][kb], a, qf[qb][dk]);
+            }
+        }
+        w64_mfma_drain();
+        sm_mask(0, S0{});
+#pragma unroll
+        for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
+        apply_rescale();
+    }
+    sync_tiles();   // every wave is done with K slot 0 before iteration 0 refills it
+    {
+        const uint32_t k1 = k_slot_base(1);
+#pragma unroll
+        for (int f = 0; f < RING; ++f) ring[f] = kfrag(k1, f);
+    }
+
+    // ---- tiles the wave computes, two per iteration (score sets 0, 1) ----
+    // (a, b, c) = (t % 3, (t+1) % 3, (t+2) % 3)
+    int sa = 0, sb = 1, sc3 = 2;
+    int t = 0;
+    for (; t < ntw2; t += 2) {
+        iteration(t, S0{}, sa, sb, sc3);
+        iteration(t + 1, S1{}, sb, sc3, sa);
+        const int tmp = sa;
+        sa = sc3;
+        sc3 = sb;
+        sb = tmp;
+    }
+    // ---- remaining tiles of the workgroup: DMAs and barriers only ----
+    for (; t < nt2; ++t) {
+#pragma unroll
+        for (int i = 0; i < 2 * LOADS; ++i) dma_step(t, sa, sc3, i);
+        sync_tiles();
+        const int tmp = sa;
+        sa = sb;
+        sb = sc3;
+        sc3 = tmp;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no DMA outlives the workgroup
+    w64_mfma_drain();
+
+    // ---- epilogue: normalise, store O, m, l ----
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
+        const int qi = q0w + 32 * qb + col;
+        if (wave_active && qi < S) {
+            const float inv = 1.0f / l_sum;
+            const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
+            T *orow = og + (int64_t)qi * p.o_ss;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int d = 32 * db + 8 * g4 + 4 * hi;
+                    u32x2_t w2 = {E::pack2(acc[qb][db][4 * g4] * inv, acc[qb][db][4 * g4 + 1] * inv),
+                                  E::pack2(acc[qb][db][4 * g4 + 2] * inv, acc[qb][db][4 * g4 + 3] * inv)};
+                    *(u32x2_t *)(orow + d) = w2;
+                }
+            if (hi == 0) {
+                const int64_t mi = (int64_t)bh * S + qi;
+                const float mval = m_true[qb] * p.scale;
+                if (p.ml_f32) {
+                    ((float *)p.m)[mi] = mval;
+                    ((float *)p.l)[mi] = l_tot;
+                } else {
+                    ((T *)p.m)[mi] = (T)mval;
+                    ((T *)p.l)[mi] = (T)l_tot;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace pmkl_amd
