@@ -35,7 +35,18 @@ sys.path.insert(0, str(ROOT))
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}   # dense MFMA, MI355X public spec
 PEAK_HBM_GBS = 8000.0
 METRIC = "causal-attn TFLOP/s on 1 MI355X, bf16 B4 H32 S4096 D128; % of MFMA peak"
-KERNEL_NAME = "attn_fwd_mfma16_kernel"
+
+
+def kernel_name(w) -> str:
+    """Kernel the C ABI dispatches for workload w (its dispatch rule, restated
+    for the bench line's label): fp32 -> the fp32 kernel; 16-bit -> the
+    64-row kernel for head_dim >= 64 and S > 128 unless PMKL_ATTN_W64=0
+    (=1 also takes it at head_dim 32), else the 8-wave kernel."""
+    if w.dtype == "fp32":
+        return "attn_fwd_f32_kernel"
+    mode = os.environ.get("PMKL_ATTN_W64")
+    w64 = (mode == "1" or (mode is None and w.D >= 64)) and w.S > 128
+    return "attn_fwd_w64_kernel" if w64 else "attn_fwd_mfma16_kernel"
 WARMUP_MIN_S = 1.0
 
 
@@ -65,12 +76,16 @@ def calibrate_copy():
     print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}))
 
 
-def read_traffic(config: str):
-    """HBM bytes per launch from profiles/pmc_<kernel>_<config>.txt, or None."""
+def read_traffic(config: str, kernel: str):
+    """HBM bytes per launch from profiles/pmc_attn_fwd_<config>.txt when that
+    summary was measured on `kernel` (its "kernel_id:" line), else None."""
     path = ROOT / "profiles" / f"pmc_attn_fwd_{config}.txt"
     if not path.exists():
         return None
     txt = path.read_text()
+    k = re.search(r"^kernel_id:\s*(\S+)", txt, re.M)
+    if k is None or k.group(1) != kernel:
+        return None
     m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
     return float(m.group(1)) if m else None
 
@@ -177,7 +192,7 @@ def main():
     value = flops * args.steps / elapsed_s / 1e12
     achieved = flops / (avg_launch_ms / 1e3) / 1e12
     peak = PEAK_TFLOPS[w.dtype]
-    traffic = read_traffic(w.name)
+    traffic = read_traffic(w.name, kernel_name(w))
 
     cpu = None if args.no_cpu else cpu_baseline(w)
     if cpu is not None:
@@ -203,7 +218,7 @@ def main():
         "pct_of_mfma_peak": round(100.0 * value / peak, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic,
-                     "kernel": KERNEL_NAME if w.dtype != "fp32" else "attn_fwd_f32_kernel",
+                     "kernel": kernel_name(w),
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
                      "hbm_GBs_algorithmic": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9, 1)},
         "cpu_baseline": cpu,

@@ -13,6 +13,8 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -73,12 +75,29 @@ KernelChoice pick16w(bool causal) {
                    : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW>,
             NW * 64, NW * 32};
 }
-bool use_w64() {
-    static const bool v = [] {
+// 64-row kernel choice: PMKL_ATTN_W64=0 never, =1 wherever it applies,
+// unset: for head_dim 64 and 128 (at 32 the 8-wave kernel is faster).
+int w64_mode() {
+    static const int v = [] {
         const char *e = getenv("PMKL_ATTN_W64");
-        return e && atoi(e) == 1;
+        return e ? (atoi(e) == 1 ? 1 : 0) : -1;
     }();
     return v;
+}
+
+// CUs of the current device (cached per device; 0 if it cannot be read).
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 template <typename T, int D>
@@ -195,11 +214,15 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     if ((rc = check_tensor("o", a->o, os, B, H, S, D, es)) != PMKL_OK) return rc;
 
     // The 64-row kernel addresses a head's whole K / V through one buffer
-    // resource with 32-bit offsets.
+    // resource with 32-bit offsets, and streams the first key tiles of its
+    // next work item during the last iterations of the current one, which
+    // needs at least three key tiles per item (S > 128).
     auto head_span_ok = [&](const int64_t *st) {
         return st[2] >= 0 && ((S - 1) * st[2] + D) * (int64_t)es < (1LL << 31);
     };
-    const bool w64 = use_w64() && a->dtype != PMKL_DTYPE_F32 && head_span_ok(ks) && head_span_ok(vs);
+    const int mode = w64_mode();
+    const bool w64 = mode != 0 && (mode == 1 || D >= 64) && a->dtype != PMKL_DTYPE_F32 && S > 128 &&
+                     head_span_ok(ks) && head_span_ok(vs);
     const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64);
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
@@ -234,7 +257,15 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     p.xcd_order = (a->dtype != PMKL_DTYPE_F32 && getenv("PMKL_ATTN_NOXCD") == nullptr && (B * H) % (a->is_causal ? 16 : 8) == 0) ? 1 : 0;
 
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(kc.fn, dim3((unsigned)(n_qtiles * B * H)), dim3(kc.threads), 0, st, p);
+    // One workgroup per work item, except the 64-row kernel: one workgroup per
+    // CU, each looping over its share of the items.
+    int64_t grid = n_qtiles * B * H;
+    if (w64) {
+        const int cus = cu_count();
+        PMKL_REQUIRE(cus > 0, PMKL_EHIP, "could not read the device's CU count");
+        grid = std::min<int64_t>(grid, cus);
+    }
+    hipLaunchKernelGGL(kc.fn, dim3((unsigned)grid), dim3(kc.threads), 0, st, p);
     hipError_t err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "kernel launch failed: %s", hipGetErrorString(err));
     return PMKL_OK;

@@ -149,16 +149,15 @@ template <int CPR> __device__ __forceinline__ int swz_v(int row) {
     }
 }
 
-// Workgroup -> (head bh, query tile qt).  Default: blockIdx.x walks all heads
+// Work item (workgroup) index L -> (head bh, query tile qt).  Default: L walks all heads
 // of one query tile at a time, longest tiles first when causal.  With
-// p.xcd_order (host sets it when B*H allows), blockIdx.x is read the way the
+// p.xcd_order (host sets it when B*H allows), L is read the way the
 // dispatcher places workgroups, round-robin over the 8 XCDs (XCD = L % 8):
 // each XCD walks its heads in pairs, longest query tile first within the pair
 // (causal), or one head at a time (non-causal).  An XCD's L2 then holds the K/V
 // of about two heads at a time while the longest tiles still start first.
 template <bool CAUSAL>
-__device__ __forceinline__ void map_workgroup(const AttnParams &p, int &bh, int &qt) {
-    const int L = blockIdx.x;
+__device__ __forceinline__ void map_index(const AttnParams &p, int L, int &bh, int &qt) {
     const int NQT = p.n_qtiles;
     if (p.xcd_order) {
         const int xcd = L & 7, k = L >> 3;
@@ -174,6 +173,10 @@ __device__ __forceinline__ void map_workgroup(const AttnParams &p, int &bh, int 
         bh = L % p.BH;
         qt = CAUSAL ? (NQT - 1 - L / p.BH) : (L / p.BH);
     }
+}
+template <bool CAUSAL>
+__device__ __forceinline__ void map_workgroup(const AttnParams &p, int &bh, int &qt) {
+    map_index<CAUSAL>(p, (int)blockIdx.x, bh, qt);
 }
 
 // ---------------------------------------------------------------------------

@@ -186,40 +186,85 @@ void attn_fwd_w64_kernel(AttnParams p) {
     const int hi = lane >> 5;
     const int col = lane & 31;
 
-    int bh, qt;
-    map_workgroup<CAUSAL>(p, bh, qt);
-    const int b = bh / p.H;
-    const int h = bh - b * p.H;
     const int S = p.S;
+    const int n_items = p.n_qtiles * p.BH;
+    // Work items (head bh, query tile qt) of this workgroup, one after the
+    // other: round r takes item index r * G + c, c running forwards in even
+    // rounds and backwards in odd ones.  Items come longest first, so the
+    // causal work evens out over the workgroups.  With p.xcd_order the snake
+    // runs over the workgroups of each XCD, keeping item index % 8 = XCD.
+    const int G = gridDim.x;
+    auto item_index = [&](int r) __attribute__((always_inline)) {
+        const int wg = blockIdx.x;
+        if (p.xcd_order && (G & 7) == 0) {
+            const int C = G >> 3, c = wg >> 3;
+            return 8 * (r * C + ((r & 1) ? C - 1 - c : c)) + (wg & 7);
+        }
+        return r * G + ((r & 1) ? G - 1 - wg : wg);
+    };
+    auto item_tiles = [&](int qt_) __attribute__((always_inline)) {
+        const int last_key = CAUSAL ? min(qt_ * kBlockM + kBlockM - 1, S - 1) : S - 1;
+        return last_key / BN + 1;   // key tiles of the item
+    };
 
-    const T *qg = (const T *)p.q + b * p.q_sb + h * p.q_sh;
-    const T *kg = (const T *)p.k + b * p.k_sb + h * p.k_sh;
-    const T *vg = (const T *)p.v + b * p.v_sb + h * p.v_sh;
-    T *og = (T *)p.o + b * p.o_sb + h * p.o_sh;
+    // Current item.
+    int bh = 0, qt = 0, q0w = 0, nt = 1, nt2 = 2, ntw = 0, ntw2 = 0;
+    bool wave_active = false;
+    const T *kg = nullptr, *vg = nullptr;
+    // Next item: its first tiles are loaded during the current item's last
+    // iterations.
+    bool has_next = false;
+    int nt_n = 1;
+    const T *kg_n = nullptr, *vg_n = nullptr;
+    auto head_ptrs = [&](int bh_, const T *&kp, const T *&vp) __attribute__((always_inline)) {
+        const int b_ = bh_ / p.H, h_ = bh_ - b_ * p.H;
+        kp = (const T *)p.k + b_ * p.k_sb + h_ * p.k_sh;
+        vp = (const T *)p.v + b_ * p.v_sb + h_ * p.v_sh;
+    };
+    auto set_item = [&](int L) __attribute__((always_inline)) {
+        map_index<CAUSAL>(p, L, bh, qt);
+        q0w = qt * kBlockM + 64 * wave;   // first row of the wave
+        nt = item_tiles(qt);
+        nt2 = (nt + 1) & ~1;              // iterations run by every wave
+        wave_active = q0w < S;
+        // Tiles this wave computes: 0 .. ntw-1; only tile ntw-1 can hold keys
+        // past a row of the wave (causal diagonal) or past S.  Rounded up to
+        // even, the extra tile being fully masked.
+        ntw = !wave_active ? 0 : CAUSAL ? min(nt, (q0w + 63) / BN + 1) : nt;
+        ntw2 = (ntw + 1) & ~1;
+        head_ptrs(bh, kg, vg);
+    };
+    auto set_next = [&](int L) __attribute__((always_inline)) {
+        has_next = L < n_items;
+        if (has_next) {
+            int bh_n, qt_n;
+            map_index<CAUSAL>(p, L, bh_n, qt_n);
+            nt_n = item_tiles(qt_n);
+            head_ptrs(bh_n, kg_n, vg_n);
+        }
+    };
 
-    const int q0 = qt * kBlockM;
-    const int q0w = q0 + 64 * wave;                   // first row of the wave
-    const int last_key = CAUSAL ? min(q0 + kBlockM - 1, S - 1) : S - 1;
-    const int nt = last_key / BN + 1;                 // key tiles of the workgroup
-    const int nt2 = (nt + 1) & ~1;                    // iterations run by every wave
-    const bool wave_active = q0w < S;
-    // Tiles this wave computes: 0 .. ntw-1; only tile ntw-1 can hold keys past
-    // a row of the wave (causal diagonal) or past S.  Rounded up to even, the
-    // extra tile being fully masked.
-    const int ntw = !wave_active ? 0 : CAUSAL ? min(nt, (q0w + 63) / BN + 1) : nt;
-    const int ntw2 = (ntw + 1) & ~1;
-
-    // Q fragments (B operand of S^T = K Q^T, AGPRs): block qb, lane holds
-    // Q[q0w + 32 qb + col][16 dk + 8 hi .. +7].
+    // Q fragments of the current item (B operand of S^T = K Q^T, AGPRs):
+    // block qb, lane holds Q[q0w + 32 qb + col][16 dk + 8 hi .. +7].
     frag qf[2][NDK];
+    auto load_q = [&]() __attribute__((always_inline)) {
+        const int b_ = bh / p.H, h_ = bh - b_ * p.H;
+        const T *qg = (const T *)p.q + b_ * p.q_sb + h_ * p.q_sh;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        const int qrow = min(q0w + 32 * qb + col, S - 1);
-        const T *src = qg + (int64_t)qrow * p.q_ss + 8 * hi;
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qrow = min(q0w + 32 * qb + col, S - 1);
+            const T *src = qg + (int64_t)qrow * p.q_ss + 8 * hi;
 #pragma unroll
-        for (int dk = 0; dk < NDK; ++dk)
-            qf[qb][dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(src + 16 * dk));
-    }
+            for (int dk = 0; dk < NDK; ++dk)
+                qf[qb][dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(src + 16 * dk));
+        }
+        // Defined in AGPRs, where the QK MFMAs read them: otherwise the
+        // register allocator may keep them in VGPRs and copy before each use.
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int dk = 0; dk < NDK; ++dk) asm volatile("" : "+a"(qf[qb][dk]));
+    };
 
     // ---- DMA staging: lane `lane` of wave `wave` fills chunk slot
     // j*256 + 64*wave + lane, i.e. LDS bytes slot_base + 4096 j + 1024 wave
@@ -233,25 +278,31 @@ void attn_fwd_w64_kernel(AttnParams p) {
         koff[j] = (int)((row * p.k_ss + 8 * (pc ^ swz_k<CPR>(row))) * (int64_t)sizeof(T));
         voff[j] = (int)((row * p.v_ss + 8 * (pc ^ swz_v<CPR>(row))) * (int64_t)sizeof(T));
     }
-    // Buffer resources of the head's K and V, from key 0 to the last key of
+    // Buffer resource of one head's K or V, from key 0 to the last key of
     // the sequence: rows past S read as zero (those keys are masked).  The
     // host keeps (S - 1) * stride + D elements within 2^31 bytes.
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)kg, (short)0, (int)(((S - 1) * p.k_ss + D) * sizeof(T)), 0x00020000);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)vg, (short)0, (int)(((S - 1) * p.v_ss + D) * sizeof(T)), 0x00020000);
+    const int k_records = (int)(((S - 1) * p.k_ss + D) * sizeof(T));
+    const int v_records = (int)(((S - 1) * p.v_ss + D) * sizeof(T));
     const int k_tile_bytes = (int)(BN * p.k_ss * sizeof(T));
     const int v_tile_bytes = (int)(BN * p.v_ss * sizeof(T));
     const unsigned lds_w = lds0 + (unsigned)(wave * 1024);
-    // DMA j of K / V tile kt (data clamped to the last tile) into LDS slot
-    // sl = kt % 3 (kept by the caller).
+    // DMA j of the K / V tile at stream position kt of the current item into
+    // LDS slot sl (= position % 3, kept by the caller).  Positions past the
+    // item's iterations (nt2) are the next item's tiles 0, 1, 2; tiles are
+    // clamped to the item's last one (the copies past it are never read).
     auto dma_k = [&](int kt, int sl, int j) __attribute__((always_inline)) {
-        w64_lds_dma16(krs, koff[j] + min(kt, nt - 1) * k_tile_bytes,
-                      lds_w + (unsigned)(sl * TILE_BYTES + j * 4096));
+        const bool nx = has_next && kt >= nt2;
+        const T *base = nx ? kg_n : kg;
+        const int tile = nx ? min(kt - nt2, nt_n - 1) : min(kt, nt - 1);
+        w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, k_records, 0x00020000),
+                      koff[j] + tile * k_tile_bytes, lds_w + (unsigned)(sl * TILE_BYTES + j * 4096));
     };
     auto dma_v = [&](int kt, int sl, int j) __attribute__((always_inline)) {
-        w64_lds_dma16(vrs, voff[j] + min(kt, nt - 1) * v_tile_bytes,
-                      lds_w + (unsigned)((3 + sl) * TILE_BYTES + j * 4096));
+        const bool nx = has_next && kt >= nt2;
+        const T *base = nx ? vg_n : vg;
+        const int tile = nx ? min(kt - nt2, nt_n - 1) : min(kt, nt - 1);
+        w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, v_records, 0x00020000),
+                      voff[j] + tile * v_tile_bytes, lds_w + (unsigned)((3 + sl) * TILE_BYTES + j * 4096));
     };
     // DMA i of iteration t: K(t+3) into slot t % 3 (sl0), then V(t+2) into
     // slot (t+2) % 3 (sl2).
@@ -267,23 +318,31 @@ void attn_fwd_w64_kernel(AttnParams p) {
         asm volatile("" ::: "memory");
     };
 
+    // Softmax state of the current item (reset per item).
     f32x16_t acc[2][NDB];      // O^T accumulators, AGPRs
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.f;
     f32x16_t sc[2][2][2];      // [set][qb][kb] scores; tile t uses set t & 1
     uint32_t pk[2][2][8];      // [qb][kb][pair] probabilities of the tile in PV
     float pe[2][2];            // exponentials of a pair until packed, by pair parity
-    float m_true[2] = {-INFINITY, -INFINITY};
-    float m_use[2] = {-INFINITY, -INFINITY};
-    float moff[2] = {0.f, 0.f};   // -m_use * scale_log2 (0 while m_use is -inf)
-    float alpha[2] = {1.f, 1.f};
-    bool rescale[2] = {false, false};
-    float l_a[2] = {0.f, 0.f}, l_b[2] = {0.f, 0.f};   // two partial row sums per block
+    float m_true[2], m_use[2];
+    float moff[2];             // -m_use * scale_log2 (0 while m_use is -inf)
+    float alpha[2];
+    bool rescale[2];
+    float l_a[2], l_b[2];      // two partial row sums per block
     const float lazy_raw = kLazyLog2 / p.scale_log2;
+    auto reset_state = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[qb][db][r] = 0.f;
+            m_true[qb] = m_use[qb] = -INFINITY;
+            moff[qb] = 0.f;
+            alpha[qb] = 1.f;
+            rescale[qb] = false;
+            l_a[qb] = l_b[qb] = 0.f;
+        }
+    };
 
     const int arow = key_of_arow(col);
     const int g16 = lane >> 4, tt = lane & 15;
@@ -326,7 +385,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     // later tiles entirely (a fully masked tile changes nothing).
     auto sm_mask = [&](int kt, auto set_c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
-        if (kt >= ntw - 1) {
+        if (__builtin_expect(kt >= ntw - 1, 0)) {
             const int kbase = kt * BN;
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
@@ -379,7 +438,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     auto apply_rescale = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
-            if (rescale[qb]) {
+            if (__builtin_expect(rescale[qb], 0)) {
                 l_a[qb] *= alpha[qb];
                 l_b[qb] *= alpha[qb];
                 w64_mfma_drain();
@@ -465,7 +524,48 @@ void attn_fwd_w64_kernel(AttnParams p) {
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
 
-    // ---- prologue: K(0), V(0), K(1) landed; K(2), V(1) in flight ----
+    // Epilogue of an item: normalise, store O, m, l.
+    auto store_item = [&](int bh_e, int q0w_e, bool active_e) __attribute__((always_inline)) {
+        const int b_ = bh_e / p.H, h_ = bh_e - b_ * p.H;
+        T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
+            const int qi = q0w_e + 32 * qb + col;
+            if (active_e && qi < S) {
+                const float inv = 1.0f / l_sum;
+                const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
+                T *orow = og + (int64_t)qi * p.o_ss;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const int d = 32 * db + 8 * g4 + 4 * hi;
+                        u32x2_t w2 = {E::pack2(acc[qb][db][4 * g4] * inv, acc[qb][db][4 * g4 + 1] * inv),
+                                      E::pack2(acc[qb][db][4 * g4 + 2] * inv, acc[qb][db][4 * g4 + 3] * inv)};
+                        *(u32x2_t *)(orow + d) = w2;
+                    }
+                if (hi == 0) {
+                    const int64_t mi = (int64_t)bh_e * S + qi;
+                    const float mval = m_true[qb] * p.scale;
+                    if (p.ml_f32) {
+                        ((float *)p.m)[mi] = mval;
+                        ((float *)p.l)[mi] = l_tot;
+                    } else {
+                        ((T *)p.m)[mi] = (T)mval;
+                        ((T *)p.l)[mi] = (T)l_tot;
+                    }
+                }
+            }
+        }
+    };
+
+    // ---- first item: K(0), V(0), K(1) landed; K(2), V(1) in flight ----
+    int r = 0;
+    if (item_index(0) >= n_items) return;   // (the host launches at most n_items workgroups)
+    set_item(item_index(0));
+    set_next(item_index(1));
+    load_q();
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         dma_k(0, 0, j);
@@ -479,88 +579,74 @@ void attn_fwd_w64_kernel(AttnParams p) {
         dma_v(1, 1, j);
     }
     sync_tiles();
-    // Scores and maxima of tile 0.
-    {
-        const uint32_t k0 = k_slot_base(0);
-#pragma unroll
-        for (int f = 0; f < NKF; ++f) {
-            const frag a = kfrag(k0, f);
-            const int dk = f >> 1, kb = f & 1;
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                if (dk == 0) M::qk0(sc[0][qb][kb], a, qf[qb][0]);
-                else M::qk(sc[0][qb][kb], a, qf[qb][dk]);
-            }
-        }
-        w64_mfma_drain();
-        sm_mask(0, S0{});
-#pragma unroll
-        for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
-        apply_rescale();
-    }
-    sync_tiles();   // every wave is done with K slot 0 before iteration 0 refills it
-    {
-        const uint32_t k1 = k_slot_base(1);
-#pragma unroll
-        for (int f = 0; f < RING; ++f) ring[f] = kfrag(k1, f);
-    }
-
-    // ---- tiles the wave computes, two per iteration (score sets 0, 1) ----
-    // (a, b, c) = (t % 3, (t+1) % 3, (t+2) % 3)
+    // LDS slots of stream positions t, t+1, t+2 of the current item; the
+    // stream runs on from item to item.
     int sa = 0, sb = 1, sc3 = 2;
-    int t = 0;
-    for (; t < ntw2; t += 2) {
-        iteration(t, S0{}, sa, sb, sc3);
-        iteration(t + 1, S1{}, sb, sc3, sa);
-        const int tmp = sa;
-        sa = sc3;
-        sc3 = sb;
-        sb = tmp;
-    }
-    // ---- remaining tiles of the workgroup: DMAs and barriers only ----
-    for (; t < nt2; ++t) {
+
+    while (true) {
+        // Scores and maxima of tile 0 (slot sa; landed, see above).
+        reset_state();
+        {
+            const uint32_t k0 = k_slot_base(sa);
 #pragma unroll
-        for (int i = 0; i < 2 * LOADS; ++i) dma_step(t, sa, sc3, i);
-        sync_tiles();
-        const int tmp = sa;
-        sa = sb;
-        sb = sc3;
-        sc3 = tmp;
+            for (int f = 0; f < NKF; ++f) {
+                const frag a = kfrag(k0, f);
+                const int dk = f >> 1, kb = f & 1;
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    if (dk == 0) M::qk0(sc[0][qb][kb], a, qf[qb][0]);
+                    else M::qk(sc[0][qb][kb], a, qf[qb][dk]);
+                }
+            }
+            w64_mfma_drain();
+            sm_mask(0, S0{});
+#pragma unroll
+            for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
+            apply_rescale();
+        }
+        sync_tiles();   // every wave is done with K slot sa before iteration 0 refills it
+        {
+            const uint32_t k1 = k_slot_base(sb);
+#pragma unroll
+            for (int f = 0; f < RING; ++f) ring[f] = kfrag(k1, f);
+        }
+
+        // ---- tiles the wave computes, two per iteration (score sets 0, 1) ----
+        int t = 0;
+        for (; t < ntw2; t += 2) {
+            iteration(t, S0{}, sa, sb, sc3);
+            iteration(t + 1, S1{}, sb, sc3, sa);
+            const int tmp = sa;
+            sa = sc3;
+            sc3 = sb;
+            sb = tmp;
+        }
+        // ---- remaining tiles of the item: DMAs and barriers only ----
+        for (; t < nt2; ++t) {
+#pragma unroll
+            for (int i = 0; i < 2 * LOADS; ++i) dma_step(t, sa, sc3, i);
+            sync_tiles();
+            const int tmp = sa;
+            sa = sb;
+            sb = sc3;
+            sc3 = tmp;
+        }
+        w64_mfma_drain();   // the last PV MFMAs have written O
+
+        // Next item first (its Q loads overlap this item's epilogue), then
+        // this item's outputs.
+        const int bh_e = bh, q0w_e = q0w;
+        const bool active_e = wave_active, more = has_next;
+        if (more) {
+            ++r;
+            set_item(item_index(r));
+            set_next(item_index(r + 1));
+            load_q();
+        }
+        store_item(bh_e, q0w_e, active_e);
+        if (!more) break;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no DMA outlives the workgroup
-    w64_mfma_drain();
-
-    // ---- epilogue: normalise, store O, m, l ----
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
-        const int qi = q0w + 32 * qb + col;
-        if (wave_active && qi < S) {
-            const float inv = 1.0f / l_sum;
-            const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
-            T *orow = og + (int64_t)qi * p.o_ss;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int d = 32 * db + 8 * g4 + 4 * hi;
-                    u32x2_t w2 = {E::pack2(acc[qb][db][4 * g4] * inv, acc[qb][db][4 * g4 + 1] * inv),
-                                  E::pack2(acc[qb][db][4 * g4 + 2] * inv, acc[qb][db][4 * g4 + 3] * inv)};
-                    *(u32x2_t *)(orow + d) = w2;
-                }
-            if (hi == 0) {
-                const int64_t mi = (int64_t)bh * S + qi;
-                const float mval = m_true[qb] * p.scale;
-                if (p.ml_f32) {
-                    ((float *)p.m)[mi] = mval;
-                    ((float *)p.l)[mi] = l_tot;
-                } else {
-                    ((T *)p.m)[mi] = (T)mval;
-                    ((T *)p.l)[mi] = (T)l_tot;
-                }
-            }
-        }
-    }
 }
 
 }  // namespace pmkl_amd

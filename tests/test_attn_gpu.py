@@ -152,6 +152,27 @@ def test_config_sampled_rows(device, name):
     assert float(o.float().abs().max()) <= vmax * (1 + 2.0 ** -7)
 
 
+@pytest.mark.parametrize("B,H,S,D,dtype,causal", [
+    (4, 64, 512, 64, "bf16", False),    # 512 items, XCD-grouped order
+    (2, 65, 512, 128, "fp16", True),    # 260 items: last round ragged, plain order
+    (1, 256, 384, 128, "bf16", True),   # 512 items, half of the last q-tile's waves idle
+])
+def test_many_items_per_workgroup(device, B, H, S, D, dtype, causal):
+    """More work items than CUs: the 64-row kernel's workgroups each run several
+    (head, query tile) items back to back, streaming the next item's first K/V
+    tiles during the current one's last iterations."""
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+
+    tag = f"{dtype} B{B} H{H} S{S} D{D} causal={causal}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=7000 + H)
+    o, m, l = _run_capi(q, k, v, device, causal=causal)
+    rows = _sample_rows(S, 16, seed=S + H)
+    errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)
+    _say(f"{tag}: {errs}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
 def test_closed_forms(device, dtype):
     """K == 0: O_i = mean(V_0..V_i), m_i = 0, l_i = i + 1 (every tile, diagonal included).
