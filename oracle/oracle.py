@@ -7,6 +7,8 @@ include/) never imports it.
 * ``attn_fwd_rows`` - ctypes call of oracle/liboracle.so, the float64
   restatement of the reference CPU operator
   (pmkl_pytorch_ext/fused_self_attention.cpp:5-64); see attn_oracle.c.
+* ``attn_bwd`` - the float64 restatement of the reference's backward
+  operator (fused_self_attention.cpp:66-135), gradients of O only.
 * ``reference_op`` - the reference's own CPU operator compiled from its source
   into oracle/_ref (oracle/Makefile), or None when that build is absent.
 * ``attn_sdpa_f64`` - torch.nn.functional.scaled_dot_product_attention in
@@ -42,6 +44,10 @@ def _lib():
                                              ctypes.c_int, ctypes.c_double, ctypes.POINTER(ctypes.c_int64),
                                              ctypes.c_int64, dp, dp, dp]
         lib.oracle_attn_fwd_rows.restype = ctypes.c_int
+        lib.oracle_attn_bwd.argtypes = [fp, fp, fp, fp, dp, dp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int, ctypes.c_double, ctypes.POINTER(ctypes.c_int64),
+                                        ctypes.c_int64, dp, dp, dp]
+        lib.oracle_attn_bwd.restype = ctypes.c_int
         _LIB = lib
     return _LIB
 
@@ -82,6 +88,37 @@ def attn_fwd_rows(q: np.ndarray, k: np.ndarray, v: np.ndarray, causal: bool = Tr
     if rc != 0:
         raise RuntimeError("oracle_attn_fwd_rows failed")
     return o, m, l
+
+
+def attn_bwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, dout: np.ndarray, m: np.ndarray, l: np.ndarray,
+             causal: bool = True, scale: float | None = None, heads=None):
+    """Float64 backward oracle (gradients of O; fused_self_attention.cpp:66-135).
+    q, k, v, dout: [BH, S, D]; m, l: [BH, S] as the forward returned them.
+    heads: None for every head, or the head indices to evaluate.
+    Returns (dq, dk, dv), each [nheads, S, D] float64."""
+    q, k, v, dout = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v, dout))
+    m = np.ascontiguousarray(m, dtype=np.float64)
+    l = np.ascontiguousarray(l, dtype=np.float64)
+    assert q.ndim == 3 and q.shape == k.shape == v.shape == dout.shape and m.shape == l.shape == q.shape[:2]
+    BH, S, D = q.shape
+    if scale is None:
+        scale = default_scale(D)
+    if heads is None:
+        NH, heads_p = BH, None
+    else:
+        heads_arr = np.ascontiguousarray(np.asarray(heads, dtype=np.int64))
+        NH = heads_arr.size
+        heads_p = heads_arr.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+    out = [np.empty((NH, S, D), dtype=np.float64) for _ in range(3)]
+    fp = ctypes.POINTER(ctypes.c_float)
+    dp = ctypes.POINTER(ctypes.c_double)
+    rc = _lib().oracle_attn_bwd(q.ctypes.data_as(fp), k.ctypes.data_as(fp), v.ctypes.data_as(fp),
+                                dout.ctypes.data_as(fp), m.ctypes.data_as(dp), l.ctypes.data_as(dp),
+                                BH, S, D, 1 if causal else 0, float(scale), heads_p, NH,
+                                *(x.ctypes.data_as(dp) for x in out))
+    if rc != 0:
+        raise RuntimeError("oracle_attn_bwd failed")
+    return tuple(out)
 
 
 def reference_op():
@@ -130,4 +167,4 @@ def ulp(x: np.ndarray, mant_bits: int) -> np.ndarray:
     return np.ldexp(1.0, (e - mant_bits).astype(np.int64))
 
 
-__all__ = ["attn_fwd_rows", "default_scale", "reference_op", "attn_sdpa_f64", "causal_flops", "ulp"]
+__all__ = ["attn_fwd_rows", "attn_bwd", "default_scale", "reference_op", "attn_sdpa_f64", "causal_flops", "ulp"]

@@ -1,4 +1,4 @@
-"""Writes the golden fixtures of the attention forward path (tests/golden/*.npz).
+"""Writes the golden fixtures of the attention path (tests/golden/*.npz).
 
 The expected outputs come from the reference's own CPU operator,
 pmkl_pytorch_ext.fused_self_attention_fw (pmkl_pytorch_ext/fused_self_attention.cpp:
@@ -16,6 +16,13 @@ Inputs are seeded (numpy PCG64) and stored once in float32; a rounded run
 takes them rounded to its dtype (torch.Tensor.to, round-to-nearest-even).
 bfloat16 outputs are stored as their uint16 bit patterns (numpy has no
 bfloat16).
+
+Backward fixtures (bwd_*.npz) come the same way from the reference's
+pmkl_pytorch_ext.fused_self_attention_bw (fused_self_attention.cpp:175-215),
+run per dtype on the m, l its own forward returned in that dtype (as the
+reference's autograd backward does, pmkl_function/__init__.py:25-32), with a
+seeded dout; the float64 case is cross-checked against torch autograd through
+scaled_dot_product_attention in float64 before it is written.
 
 Run from the repository root in a container that holds /root/reference:
     make -C oracle && python tests/golden/gen_golden.py
@@ -61,6 +68,16 @@ def inputs(B, H, S, D, seed, dist):
     return [a.astype(np.float32) for a in arrs]
 
 
+# (name, B, H, S, D, causal, seed) of the backward fixtures (the reference's
+# backward is O(S^3 D), so they stay small)
+BWD_CASES = [
+    ("s37_d64_causal", 1, 2, 37, 64, True, 21),
+    ("s37_d64_full", 1, 1, 37, 64, False, 22),
+    ("s48_d128_causal", 1, 1, 48, 128, True, 23),
+    ("s20_d32_causal", 2, 1, 20, 32, True, 24),
+]
+
+
 def as_store(t: torch.Tensor) -> np.ndarray:
     if t.dtype == torch.bfloat16:
         return t.contiguous().view(torch.int16).numpy().view(np.uint16)
@@ -88,6 +105,31 @@ def main():
             rec[f"m_{dt}"] = as_store(m)
             rec[f"l_{dt}"] = as_store(l)
         path = OUT / f"ref_{name}.npz"
+        np.savez_compressed(path, **rec)
+        print(f"wrote {path.relative_to(ROOT)} ({path.stat().st_size} bytes)")
+    for name, B, H, S, D, causal, seed in BWD_CASES:
+        q, k, v = inputs(B, H, S, D, seed, "normal")
+        dout = np.random.Generator(np.random.PCG64(seed + 1000)).standard_normal((B, H, S, D)).astype(np.float32)
+        rec = {"B": B, "H": H, "S": S, "D": D, "causal": int(causal), "seed": seed,
+               "q": q, "k": k, "v": v, "dout": dout}
+        for dt, tdt in TORCH.items():
+            qt, kt, vt, dot = (torch.from_numpy(a).to(tdt) for a in (q, k, v, dout))
+            o, m, l = ref.fused_self_attention_fw(qt, kt, vt, causal)
+            dq, dk, dv = ref.fused_self_attention_bw(dot, qt, kt, vt, m, l, causal)
+            if dt == "fp64":
+                ts = [torch.from_numpy(a.astype(np.float64)).requires_grad_() for a in (q, k, v)]
+                ot = torch.nn.functional.scaled_dot_product_attention(
+                    *ts, is_causal=causal, scale=oracle.default_scale(D))
+                ot.backward(torch.from_numpy(dout.astype(np.float64)))
+                for g, t in zip((dq, dk, dv), ts):
+                    err = (g - t.grad).abs().max().item()
+                    assert err < 1e-11, f"{name}: reference fp64 backward vs SDPA autograd differ by {err}"
+            rec[f"m_{dt}"] = as_store(m)
+            rec[f"l_{dt}"] = as_store(l)
+            rec[f"dq_{dt}"] = as_store(dq)
+            rec[f"dk_{dt}"] = as_store(dk)
+            rec[f"dv_{dt}"] = as_store(dv)
+        path = OUT / f"bwd_{name}.npz"
         np.savez_compressed(path, **rec)
         print(f"wrote {path.relative_to(ROOT)} ({path.stat().st_size} bytes)")
 
