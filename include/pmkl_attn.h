@@ -1,5 +1,6 @@
 /*
- * pmkl_attn.h - C ABI of the MI355X (gfx950) fused causal self-attention forward.
+ * pmkl_attn.h - C ABI of the MI355X (gfx950) fused causal self-attention
+ * forward and its backward.
  *
  * This is the drop-in boundary for the pmkl hot path.  Every entry point takes
  * plain pointers and sizes; no C++, HIP or torch type crosses it (the stream is
@@ -11,6 +12,9 @@
  *       -> reference pmkl/nlp/causal_attention.h:258-288
  *   fused_self_attention_fw(q, k, v, is_causal) -> (out, out_m, out_l)
  *       -> reference pmkl_pytorch_ext/fused_self_attention.cpp:139-173
+ *   fused_self_attention_bw(dout, q, k, v, out_m, out_l, is_causal) -> (dq, dk, dv)
+ *       -> reference pmkl_pytorch_ext/fused_self_attention.cpp:175-215
+ *          (algorithm :66-135)
  *
  * Semantics (identical to the reference CPU operator,
  * fused_self_attention.cpp:5-64, evaluated with fp32 accumulation):
@@ -23,8 +27,8 @@
  * are contiguous [batch, heads, seq].
  *
  * Contract:
- *   - The caller allocates q, k, v, o, m, l in device memory; the library
- *     allocates nothing per call.
+ *   - The caller allocates every tensor (and the backward's workspace) in
+ *     device memory; the library allocates nothing per call.
  *   - Calls are asynchronous on the given stream (NULL = the default stream).
  *   - The functions are re-entrant and thread-safe; error text is thread-local.
  */
@@ -37,7 +41,7 @@
 extern "C" {
 #endif
 
-#define PMKL_ABI_VERSION 1
+#define PMKL_ABI_VERSION 2
 
 /* Element types.  The reference dispatches on float, double, half and
  * bfloat16 (fused_self_attention.cpp:152-156); the device path implements
@@ -96,6 +100,52 @@ int pmkl_causal_attention_forward(int32_t dtype, void *out, const void *q, const
 
 /* 1 if a kernel is compiled for (dtype, head_dim), else 0. */
 int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim);
+
+/* Arguments of pmkl_attn_bwd.  All tensors contiguous [B, H, S, D] (m, l:
+ * [B, H, S]), as the reference operator requires (fused_self_attention.cpp:
+ * 181-182 checks q, k, v contiguous and makes dout contiguous).
+ * Gradients of O only, as the reference: with the forward's m and l,
+ *   P_ij  = exp(s_ij - m_i) / l_i,   dP_ij = <dout_i, v_j>,
+ *   dS_ij = P_ij (dP_ij - sum_j' P_ij' dP_ij'),
+ *   dq_i = scale sum_j dS_ij k_j,  dk_j = scale sum_i dS_ij q_i,
+ *   dv_j = sum_i P_ij dout_i. */
+typedef struct pmkl_attn_bwd_args {
+    const void *dout;
+    const void *q;
+    const void *k;
+    const void *v;
+    const void *o;       /* optional forward output: with it sum_j' P dP is
+                            <dout_i, o_i>; NULL computes it from the keys      */
+    const void *m;       /* [B, H, S] as pmkl_attn_fwd returned it             */
+    const void *l;
+    void *dq;
+    void *dk;
+    void *dv;
+    void *workspace;     /* device memory, 16-byte aligned, at least
+                            pmkl_attn_bwd_workspace_size() bytes; scratch of
+                            the call (two floats per query row)               */
+    uint64_t workspace_bytes;
+    int32_t dtype;       /* pmkl_dtype of dout, q, k, v, o, dq, dk, dv: F16 or BF16 */
+    int32_t ml_dtype;    /* pmkl_dtype of m and l: dtype or F32                 */
+    int64_t batch;
+    int64_t heads;
+    int64_t seq_len;
+    int64_t head_dim;    /* 32, 64 or 128                                        */
+    float scale;         /* 0 -> 1.0f / sqrtf((float)head_dim)                   */
+    int32_t is_causal;
+} pmkl_attn_bwd_args;
+
+/* Bytes of workspace pmkl_attn_bwd needs for this shape. */
+uint64_t pmkl_attn_bwd_workspace_size(int64_t batch, int64_t heads, int64_t seq_len);
+
+/* Backward of the attention output.  Replaces the device half of
+ * fused_self_attention_bw (fused_self_attention.cpp:175-215), whose
+ * algorithm is :66-135.  Writes dq, dk, dv (every element).  Asynchronous on
+ * `stream`; allocates nothing.  Returns a pmkl_status. */
+int pmkl_attn_bwd(const pmkl_attn_bwd_args *args, void *stream);
+
+/* 1 if a backward kernel is compiled for (dtype, head_dim), else 0. */
+int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim);
 
 /* Thread-local text of the last error ("" if none), with the file:line of the
  * check that failed, in the style of the reference's CHECK_FAIL message. */

@@ -13,7 +13,7 @@ from __future__ import annotations
 
 from . import capi
 
-__all__ = ["attn_fwd", "capi", "torch_dtype_to_pmkl"]
+__all__ = ["attn_fwd", "attn_bwd", "capi", "torch_dtype_to_pmkl"]
 
 
 def torch_dtype_to_pmkl(dt) -> int:
@@ -64,3 +64,48 @@ def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dty
     if rc != capi.PMKL_OK:
         raise capi.PmklError(rc, capi.last_error())
     return out, out_m, out_l
+
+
+def attn_bwd(dout, q, k, v, out_m, out_l, is_causal: bool = True, scale: float | None = None, out=None,
+             stream=None):
+    """Backward of the attention output on ROCm tensors through pmkl_attn_bwd.
+
+    dout, q, k, v: contiguous [B, H, S, D] (fp16 / bf16); out_m, out_l: the
+    forward's [B, H, S] outputs (in q's dtype or float32).  `out` (the
+    forward's O) is optional: with it the row terms come from <dout, O>.
+    Returns (dq, dk, dv).  Runs on `stream` or torch's current stream; the
+    workspace is allocated through torch's caching allocator.
+    """
+    import torch
+
+    for name, t in (("dout", dout), ("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise ValueError(f"attn_bwd takes ROCm device tensors ({name} is not)")
+        if t.dim() != 4 or t.shape != q.shape:
+            raise ValueError("dout, q, k, v must share a 4-D shape [B, H, S, D]")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if out is not None and (out.shape != q.shape or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous [B, H, S, D] tensor")
+    if out_m.shape != q.shape[:3] or out_l.shape != q.shape[:3] or not (out_m.is_contiguous() and out_l.is_contiguous()):
+        raise ValueError("out_m / out_l must be contiguous [B, H, S] tensors")
+    B, H, S, D = q.shape
+    dt = torch_dtype_to_pmkl(q.dtype)
+    mdt = torch_dtype_to_pmkl(out_m.dtype)
+    lib = capi.load()
+    ws_bytes = int(lib.pmkl_attn_bwd_workspace_size(B, H, S))
+    ws = torch.empty((max(ws_bytes, 16) + 3) // 4, dtype=torch.float32, device=q.device)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    a = capi.make_bwd_args(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                           0 if out is None else out.data_ptr(), out_m.data_ptr(),
+                           out_l.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                           ws.data_ptr(), ws.numel() * 4, dtype=dt, ml_dtype=mdt, batch=B, heads=H, seq_len=S,
+                           head_dim=D, is_causal=is_causal, scale=0.0 if scale is None else float(scale))
+    rc = capi.attn_bwd_raw(a, stream)
+    if rc != capi.PMKL_OK:
+        raise capi.PmklError(rc, capi.last_error())
+    return dq, dk, dv

@@ -25,6 +25,9 @@ EXPORTED_SYMBOLS = (
     "pmkl_attn_fwd",
     "pmkl_causal_attention_forward",
     "pmkl_attn_fwd_supported",
+    "pmkl_attn_bwd_workspace_size",
+    "pmkl_attn_bwd",
+    "pmkl_attn_bwd_supported",
     "pmkl_last_error",
     "pmkl_abi_version",
 )
@@ -50,6 +53,33 @@ class AttnFwdArgs(ctypes.Structure):
         ("k_strides", ctypes.c_int64 * 3),
         ("v_strides", ctypes.c_int64 * 3),
         ("o_strides", ctypes.c_int64 * 3),
+        ("scale", ctypes.c_float),
+        ("is_causal", ctypes.c_int32),
+    ]
+
+
+class AttnBwdArgs(ctypes.Structure):
+    """Mirror of pmkl_attn_bwd_args."""
+
+    _fields_ = [
+        ("dout", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("m", ctypes.c_void_p),
+        ("l", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("dtype", ctypes.c_int32),
+        ("ml_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("seq_len", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
         ("scale", ctypes.c_float),
         ("is_causal", ctypes.c_int32),
     ]
@@ -86,6 +116,12 @@ def load() -> ctypes.CDLL:
     lib.pmkl_last_error.restype = ctypes.c_char_p
     lib.pmkl_abi_version.argtypes = []
     lib.pmkl_abi_version.restype = ctypes.c_int
+    lib.pmkl_attn_bwd_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    lib.pmkl_attn_bwd_workspace_size.restype = ctypes.c_uint64
+    lib.pmkl_attn_bwd.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_void_p]
+    lib.pmkl_attn_bwd.restype = ctypes.c_int
+    lib.pmkl_attn_bwd_supported.argtypes = [ctypes.c_int32, ctypes.c_int64]
+    lib.pmkl_attn_bwd_supported.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -116,6 +152,27 @@ def make_args(q, k, v, o, m, l, *, dtype: int, ml_dtype: int | None = None, batc
     a.k_strides[:] = list(k_strides)
     a.v_strides[:] = list(v_strides)
     a.o_strides[:] = list(o_strides)
+    a.scale = scale
+    a.is_causal = 1 if is_causal else 0
+    return a
+
+
+def attn_bwd_raw(args: AttnBwdArgs, stream: int | None = None) -> int:
+    """Call pmkl_attn_bwd; returns the status code."""
+    return load().pmkl_attn_bwd(ctypes.byref(args), ctypes.c_void_p(stream or 0))
+
+
+def make_bwd_args(dout, q, k, v, o, m, l, dq, dk, dv, workspace, workspace_bytes, *, dtype: int,
+                  ml_dtype: int | None = None, batch: int, heads: int, seq_len: int, head_dim: int,
+                  is_causal: bool = True, scale: float = 0.0) -> AttnBwdArgs:
+    """Build an AttnBwdArgs from raw integer pointers (o may be 0)."""
+    a = AttnBwdArgs()
+    a.dout, a.q, a.k, a.v, a.o, a.m, a.l = dout, q, k, v, o, m, l
+    a.dq, a.dk, a.dv = dq, dk, dv
+    a.workspace, a.workspace_bytes = workspace, workspace_bytes
+    a.dtype = dtype
+    a.ml_dtype = dtype if ml_dtype is None else ml_dtype
+    a.batch, a.heads, a.seq_len, a.head_dim = batch, heads, seq_len, head_dim
     a.scale = scale
     a.is_causal = 1 if is_causal else 0
     return a

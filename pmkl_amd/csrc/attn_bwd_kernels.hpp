@@ -1,0 +1,536 @@
+// gfx950 (CDNA4) kernels of the fused self-attention backward (gradients of O).
+//
+// Reference: pmkl_pytorch_ext/fused_self_attention.cpp:66-135
+// (host_self_attention_backward, reached through fused_self_attention_bw,
+// :175-215, and the autograd backward of pmkl_function/__init__.py:25-32).
+// For every head, query n and key j, with the m, l the forward returned:
+//   P_nj  = exp(s_nj * scale - m_n) / l_n        (0 where masked)
+//   dP_nj = dout_n . v_j
+//   dS_nj = P_nj * (dP_nj - D_n),   D_n = sum_j P_nj dP_nj
+//   dq_n  = scale * sum_j dS_nj k_j,   dk_j = scale * sum_n dS_nj q_n,
+//   dv_j  = sum_n P_nj dout_n
+// which is the reference's per-(n, j) sum (:101-124) regrouped.
+//
+// Two passes, neither with atomics:
+//   attn_bwd_dq_kernel    a workgroup owns 32 query rows per wave;
+//                         K and V tiles of 64 keys stream through LDS.  One
+//                         loop over the keys gives D_n (skipped when the
+//                         caller passes O: D_n = dout_n . o_n), a second one
+//                         dS and dQ.  D_n and log2-sum-exp of every row go to
+//                         the caller's workspace for the second pass.
+//   attn_bwd_dkdv_kernel  a workgroup owns 32 key rows per wave; Q, dO tiles of 64
+//                         queries and their two row vectors stream through
+//                         LDS; dK, dV accumulate in registers.
+// Both use the forward's layouts (attn_fwd_kernels.hpp): transposed products
+// with the owned rows as the MFMA column, the A-row permutation key_of_arow
+// so that a lane half owns 16 consecutive streamed rows, P and dS packed
+// straight into the B operand of the next product, and the LDS transpose read
+// ds_read_b64_tr_b16 for operands needed with the other orientation.  A
+// streamed tensor read both as rows and transposed is kept in LDS twice, once
+// per swizzle, so both reads are bank-conflict free.
+#pragma once
+
+#include "attn_fwd_kernels.hpp"
+
+namespace pmkl_amd {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct BwdParams {
+    const void *q, *k, *v, *o, *dout;   // [BH, S, D] contiguous; o may be null
+    const void *m, *l;                  // [BH, S], the forward's outputs
+    void *dq, *dk, *dv;                 // [BH, S, D]
+    float *lse2;                        // workspace [BH, S]: m * log2(e) + log2(l)
+    float *drow;                        // workspace [BH, S]: D_n
+    int32_t S, BH;
+    int32_t n_qtiles, n_ktiles;         // ceil(S / owned rows per workgroup)
+    float scale, scale_log2;
+    int32_t ml_f32;                     // m, l stored as float (else in T)
+};
+
+// Waves per workgroup: 8 (two per SIMD) where the registers of a wave fit in
+// 256; at head_dim 128 the owned rows' fragments and the dK/dV accumulators
+// need more, so 4 waves (one per SIMD, up to 512 registers).
+template <int D> constexpr int bwd_waves() { return D >= 128 ? 4 : 8; }
+
+// 16-byte chunk (logical chunk pc of row `row`) staging of a 64-row tile:
+// loads go to registers two tiles ahead, LDS writes place the chunk at its
+// swizzled position in each layout the tensor is read with.
+template <typename T, int D>
+struct BwdTile {
+    static constexpr int NW = bwd_waves<D>();
+    static constexpr int THREADS = NW * 64;
+    static constexpr int ROWS = 32 * NW;        // owned rows per workgroup
+    static constexpr int BN = 64;
+    static constexpr int CPR = D / 8;
+    static constexpr int CHUNKS = BN * CPR;
+    static constexpr int LOADS = (CHUNKS + THREADS - 1) / THREADS;
+    static constexpr bool PARTIAL = CHUNKS % THREADS != 0;
+};
+
+// Buffer resource of the rows [r0, S) of a [S, D] matrix: rows past S read as
+// zero.
+template <typename T, int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bwd_rows_rsrc(const T *base, int r0, int S) {
+    const int rows = min(64, S - r0);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (int64_t)r0 * D), (short)0,
+                                             (int)((rows - 1) * D + D) * (int)sizeof(T), 0x00020000);
+}
+
+// A-operand fragment (rows) of a 32-row block from a tile stored with swz_k:
+// lane reads row 32 blk + key_of_arow(col), head_dim 16 dk + 8 hi .. +7.
+template <typename T, int D>
+__device__ __forceinline__ typename Elt16<T>::frag bwd_row_frag(const T *tile, int blk, int dk, int arow, int hi) {
+    constexpr int CPR = D / 8;
+    const int row = 32 * blk + arow;
+    const int x = 2 * dk + hi;
+    return __builtin_bit_cast(typename Elt16<T>::frag,
+                              *(const u32x4_t *)(tile + row * D + 8 * (x ^ swz_k<CPR>(row))));
+}
+
+// A-operand fragment of the transpose (head_dim x 16 streamed rows) from a
+// tile stored with swz_v: 32 head-dim columns 32 db .., streamed rows of the
+// 16-row block c of the 32-row block blk, in the order that matches a B
+// operand packed from registers 8c .. 8c+7 of the key_of_arow layout.
+template <typename T, int D>
+__device__ __forceinline__ typename Elt16<T>::frag bwd_tr_frag(const T *tile, int blk, int c, int db, int vrow0,
+                                                               int vcol0) {
+    constexpr int CPR = D / 8;
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    typedef short s16x8_t __attribute__((ext_vector_type(8)));
+    const int r0 = 32 * blk + 8 * c + vrow0;
+    const int cc = 32 * db + vcol0;
+    const int ch = cc >> 3, part = cc & 7;
+    const T *a0 = tile + r0 * D + 8 * (ch ^ swz_v<CPR>(r0)) + part;
+    const T *a1 = tile + (r0 + 4) * D + 8 * (ch ^ swz_v<CPR>(r0 + 4)) + part;
+    s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a0);
+    s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a1);
+    return __builtin_bit_cast(typename Elt16<T>::frag,
+                              s16x8_t{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]});
+}
+
+template <typename T>
+__device__ __forceinline__ float bwd_load_ml(const void *base, int64_t i, bool f32) {
+    return f32 ? ((const float *)base)[i] : (float)((const T *)base)[i];
+}
+
+// ---------------------------------------------------------------------------
+// pass 1: dQ (and the row vectors D_n, log2-sum-exp)
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(BwdParams p) {
+    using E = Elt16<T>;
+    using frag = typename E::frag;
+    using TL = BwdTile<T, D>;
+    constexpr int BN = TL::BN, CPR = TL::CPR, LOADS = TL::LOADS;
+    constexpr int kBwdThreads = TL::THREADS, kBwdRows = TL::ROWS;
+    constexpr bool PARTIAL = TL::PARTIAL;
+    constexpr int NDB = D / 32, NDK = D / 16;
+
+    __shared__ __attribute__((aligned(16))) T smem[2][3][BN * D];   // [stage][K swz_k, K swz_v, V swz_k]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int col = lane & 31;
+
+    // Longest query tiles first (causal).
+    const int bh = blockIdx.x % p.BH;
+    const int qt = CAUSAL ? p.n_qtiles - 1 - (int)blockIdx.x / p.BH : (int)blockIdx.x / p.BH;
+    const int S = p.S;
+    const int64_t hoff = (int64_t)bh * S * D;
+    const T *qg = (const T *)p.q + hoff;
+    const T *kg = (const T *)p.k + hoff;
+    const T *vg = (const T *)p.v + hoff;
+    const T *dog = (const T *)p.dout + hoff;
+    T *dqg = (T *)p.dq + hoff;
+
+    const int q0 = qt * kBwdRows;
+    const int q0w = q0 + 32 * wave;
+    const int qi = q0w + col;                 // this lane's query row
+    const int qrow = min(qi, S - 1);
+    const int last_key = CAUSAL ? min(q0 + kBwdRows - 1, S - 1) : S - 1;
+    const int nt = last_key / BN + 1;
+    const bool wave_active = q0w < S;
+
+    // B-operand fragments of the owned rows: Q (for S^T = K Q^T) and dout
+    // (for dP^T = V dout^T); lane holds row qi, head_dim 16 dk + 8 hi .. +7.
+    frag qf[NDK], df[NDK];
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+        qf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(qg + (int64_t)qrow * D + 16 * dk + 8 * hi));
+        df[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(dog + (int64_t)qrow * D + 16 * dk + 8 * hi));
+    }
+    // log2-sum-exp of the row: P = exp2(s * scale * log2(e) - lse2).
+    const float m_i = bwd_load_ml<T>(p.m, (int64_t)bh * S + qrow, p.ml_f32 != 0);
+    const float l_i = bwd_load_ml<T>(p.l, (int64_t)bh * S + qrow, p.ml_f32 != 0);
+    const float lse2 = m_i * 1.4426950408889634f + __log2f(l_i);
+    const float c = p.scale_log2;
+
+    // ---- staging ----
+    u32x4_t kreg[2][LOADS], vreg[2][LOADS];
+    int goff[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int sl = j * kBwdThreads + tid;
+        goff[j] = ((sl / CPR) * D + 8 * (sl % CPR)) * (int)sizeof(T);
+    }
+    auto gload = [&](int kt, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S);
+        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S);
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j)
+            if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
+                kreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[j], 0, 0));
+                vreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[j], 0, 0));
+            }
+    };
+    auto swrite = [&](int st, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int sl = j * kBwdThreads + tid;
+            if (!PARTIAL || sl < TL::CHUNKS) {
+                const int row = sl / CPR, pc = sl % CPR;
+                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = kreg[SET][j];
+                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = kreg[SET][j];
+                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = vreg[SET][j];
+            }
+        }
+    };
+
+    const int arow = key_of_arow(col);
+    const int g16 = lane >> 4, tt = lane & 15;
+    const int vrow0 = 16 * (g16 >> 1) + (tt >> 2);
+    const int vcol0 = 16 * (g16 & 1) + 4 * (tt & 3);
+
+    float drow_part = 0.f;      // pass A: per-lane part of D_n
+    float drow = 0.f;
+    f32x16_t acc[NDB];          // dQ^T (head_dim x owned rows)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+
+    // One loop over the key tiles.  PASS 0: D_n; PASS 1: dS and dQ.
+    auto key_loop = [&](auto pass_c) __attribute__((always_inline)) {
+        constexpr int PASS = decltype(pass_c)::value;
+        gload(0, std::integral_constant<int, 0>{});
+        swrite(0, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_s_waitcnt(0);
+        gload(min(1, nt - 1), std::integral_constant<int, 1>{});
+        __syncthreads();
+        auto tile_step = [&](auto set_c, int kt) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+            gload(min(kt + 2, nt - 1), set_c);
+            const int kbase = kt * BN;
+            const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
+            if (wave_needed) {
+                const T *Kk = smem[SET][0];
+                const T *Kv = smem[SET][1];
+                const T *Vk = smem[SET][2];
+                f32x16_t s[2], dp[2];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[kb][r] = dp[kb][r] = 0.f;
+#pragma unroll
+                    for (int dk = 0; dk < NDK; ++dk) {
+                        s[kb] = E::mma(bwd_row_frag<T, D>(Kk, kb, dk, arow, hi), qf[dk], s[kb]);
+                        dp[kb] = E::mma(bwd_row_frag<T, D>(Vk, kb, dk, arow, hi), df[dk], dp[kb]);
+                    }
+                }
+                // register r of block kb holds key kbase + 32 kb + 16 hi + r
+                const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+                const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
+                uint32_t dsk[2][8];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        float pv[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int key = kbase + 32 * kb + 16 * hi + r + e;
+                            const float sv = need_mask && key > lim ? -INFINITY : s[kb][r + e];
+                            pv[e] = fast_exp2(__builtin_fmaf(sv, c, -lse2));
+                        }
+                        if (PASS == 0) {
+                            drow_part = __builtin_fmaf(pv[0], dp[kb][r], drow_part);
+                            drow_part = __builtin_fmaf(pv[1], dp[kb][r + 1], drow_part);
+                        } else {
+                            dsk[kb][r >> 1] = E::pack2(pv[0] * (dp[kb][r] - drow), pv[1] * (dp[kb][r + 1] - drow));
+                        }
+                    }
+                if (PASS == 1) {
+                    // dQ^T += K^T dS^T over the 4 blocks of 16 keys
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int cc = 0; cc < 2; ++cc) {
+                            u32x4_t bw = {dsk[kb][4 * cc], dsk[kb][4 * cc + 1], dsk[kb][4 * cc + 2], dsk[kb][4 * cc + 3]};
+                            const frag bfr = __builtin_bit_cast(frag, bw);
+#pragma unroll
+                            for (int db = 0; db < NDB; ++db)
+                                acc[db] = E::mma(bwd_tr_frag<T, D>(Kv, kb, cc, db, vrow0, vcol0), bfr, acc[db]);
+                        }
+                }
+            }
+            if (kt + 1 < nt) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
+            __syncthreads();
+        };
+        for (int kt = 0; kt < nt; kt += 2) {
+            tile_step(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < nt) tile_step(std::integral_constant<int, 1>{}, kt + 1);
+        }
+    };
+
+    if (p.o != nullptr) {
+        // D_n = dout_n . o_n straight from O (same lane split as the fragments)
+        const T *og = (const T *)p.o + hoff;
+        float part = 0.f;
+#pragma unroll
+        for (int dk = 0; dk < NDK; ++dk) {
+            const frag of = __builtin_bit_cast(frag, *(const u32x4_t *)(og + (int64_t)qrow * D + 16 * dk + 8 * hi));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part = __builtin_fmaf((float)of[e], (float)df[dk][e], part);
+        }
+        drow = half_sum(part);
+    } else {
+        key_loop(std::integral_constant<int, 0>{});
+        drow = half_sum(drow_part);
+    }
+    if (hi == 0 && qi < S) {
+        p.lse2[(int64_t)bh * S + qi] = lse2;
+        p.drow[(int64_t)bh * S + qi] = drow;
+    }
+    key_loop(std::integral_constant<int, 1>{});
+
+    // ---- epilogue: dq = scale * dQ^T, lane = query column ----
+    if (wave_active && qi < S) {
+        T *row = dqg + (int64_t)qi * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * db + 8 * g4 + 4 * hi;
+                u32x2_t w2 = {E::pack2(acc[db][4 * g4] * p.scale, acc[db][4 * g4 + 1] * p.scale),
+                              E::pack2(acc[db][4 * g4 + 2] * p.scale, acc[db][4 * g4 + 3] * p.scale)};
+                *(u32x2_t *)(row + d) = w2;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// pass 2: dK, dV
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dkdv_kernel(BwdParams p) {
+    using E = Elt16<T>;
+    using frag = typename E::frag;
+    using TL = BwdTile<T, D>;
+    constexpr int BN = TL::BN, CPR = TL::CPR, LOADS = TL::LOADS;
+    constexpr int kBwdThreads = TL::THREADS, kBwdRows = TL::ROWS;
+    constexpr bool PARTIAL = TL::PARTIAL;
+    constexpr int NDB = D / 32, NDK = D / 16;
+
+    // [stage][Q swz_k, Q swz_v, dout swz_k, dout swz_v]; row vectors [stage][lse2, D_n]
+    __shared__ __attribute__((aligned(16))) T smem[2][4][BN * D];
+    __shared__ __attribute__((aligned(16))) float svec[2][2][BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int col = lane & 31;
+
+    // Key tiles with the most queries first (causal: the first keys).
+    const int bh = blockIdx.x % p.BH;
+    const int ktile = (int)blockIdx.x / p.BH;
+    const int S = p.S;
+    const int64_t hoff = (int64_t)bh * S * D;
+    const T *qg = (const T *)p.q + hoff;
+    const T *kg = (const T *)p.k + hoff;
+    const T *vg = (const T *)p.v + hoff;
+    const T *dog = (const T *)p.dout + hoff;
+    const float *lse2g = p.lse2 + (int64_t)bh * S;
+    const float *drowg = p.drow + (int64_t)bh * S;
+    T *dkg = (T *)p.dk + hoff;
+    T *dvg = (T *)p.dv + hoff;
+
+    const int k0 = ktile * kBwdRows;
+    const int k0w = k0 + 32 * wave;
+    const int kj = k0w + col;                 // this lane's key row
+    const int krow = min(kj, S - 1);
+    const bool wave_active = k0w < S;
+    const int t0 = CAUSAL ? k0 / BN : 0;      // first query tile with a visible query
+    const int nq = (S + BN - 1) / BN;
+
+    // B-operand fragments of the owned rows: K (for S = Q K^T) and V (for
+    // dP = dout V^T); lane holds row kj, head_dim 16 dk + 8 hi .. +7.
+    frag kf[NDK], vf[NDK];
+#pragma unroll
+    for (int dk = 0; dk < NDK; ++dk) {
+        kf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(kg + (int64_t)krow * D + 16 * dk + 8 * hi));
+        vf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(vg + (int64_t)krow * D + 16 * dk + 8 * hi));
+    }
+    const float c = p.scale_log2;
+
+    // ---- staging of Q, dout (two layouts each) and the row vectors ----
+    u32x4_t qreg[2][LOADS], oreg[2][LOADS];
+    float vreg[2];   // one row-vector element per thread (threads 0..127)
+    int goff[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int sl = j * kBwdThreads + tid;
+        goff[j] = ((sl / CPR) * D + 8 * (sl % CPR)) * (int)sizeof(T);
+    }
+    auto gload = [&](int qtl, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        const auto qr = bwd_rows_rsrc<T, D>(qg, qtl * BN, S);
+        const auto orr = bwd_rows_rsrc<T, D>(dog, qtl * BN, S);
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j)
+            if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
+                qreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qr, goff[j], 0, 0));
+                oreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(orr, goff[j], 0, 0));
+            }
+        if (tid < 2 * BN) {
+            const int row = qtl * BN + (tid & (BN - 1));
+            // rows past S: lse2 = +inf gives P = 0 (their scores are masked too)
+            vreg[SET] = row < S ? ((tid < BN) ? lse2g[row] : drowg[row]) : ((tid < BN) ? INFINITY : 0.f);
+        }
+    };
+    auto swrite = [&](int st, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int sl = j * kBwdThreads + tid;
+            if (!PARTIAL || sl < TL::CHUNKS) {
+                const int row = sl / CPR, pc = sl % CPR;
+                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = qreg[SET][j];
+                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = qreg[SET][j];
+                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = oreg[SET][j];
+                *(u32x4_t *)(&smem[st][3][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = oreg[SET][j];
+            }
+        }
+        if (tid < 2 * BN) svec[st][tid >> 6][tid & (BN - 1)] = vreg[SET];
+    };
+
+    const int arow = key_of_arow(col);
+    const int g16 = lane >> 4, tt = lane & 15;
+    const int vrow0 = 16 * (g16 >> 1) + (tt >> 2);
+    const int vcol0 = 16 * (g16 & 1) + 4 * (tt & 3);
+
+    f32x16_t dk_acc[NDB], dv_acc[NDB];   // dK^T, dV^T (head_dim x owned keys)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dk_acc[db][r] = dv_acc[db][r] = 0.f;
+
+    const int ntl = nq - t0;   // query tiles of the workgroup
+    if (ntl > 0) {
+        gload(t0, std::integral_constant<int, 0>{});
+        swrite(0, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_s_waitcnt(0);
+        gload(min(t0 + 1, nq - 1), std::integral_constant<int, 1>{});
+        __syncthreads();
+    }
+    auto tile_step = [&](auto set_c, int it) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
+        const int qtl = t0 + it;
+        gload(min(qtl + 2, nq - 1), set_c);
+        const int qbase = qtl * BN;
+        // causal: the tile holds a query at or past the wave's first key
+        const bool wave_needed = wave_active && (!CAUSAL || qbase + BN - 1 >= k0w);
+        if (wave_needed) {
+            const T *Qk = smem[SET][0];
+            const T *Qv = smem[SET][1];
+            const T *Ok = smem[SET][2];
+            const T *Ov = smem[SET][3];
+            const float *lse2s = svec[SET][0];
+            const float *drows = svec[SET][1];
+            f32x16_t s[2], dp[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[qb][r] = dp[qb][r] = 0.f;
+#pragma unroll
+                for (int dk = 0; dk < NDK; ++dk) {
+                    s[qb] = E::mma(bwd_row_frag<T, D>(Qk, qb, dk, arow, hi), kf[dk], s[qb]);
+                    dp[qb] = E::mma(bwd_row_frag<T, D>(Ok, qb, dk, arow, hi), vf[dk], dp[qb]);
+                }
+            }
+            // register r of block qb holds query qbase + 32 qb + 16 hi + r
+            const bool need_mask = (CAUSAL && qbase < k0w + 31) || (qbase + BN > S);
+            uint32_t pp[2][8], dsp[2][8];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                const int rb = 32 * qb + 16 * hi;
+                f32x4_t l4[4], d4[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    l4[i] = *(const f32x4_t *)(lse2s + rb + 4 * i);
+                    d4[i] = *(const f32x4_t *)(drows + rb + 4 * i);
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    float pv[2], dsv[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int q = qbase + rb + r + e;
+                        const bool vis = !need_mask || (q < S && (!CAUSAL || q >= kj));
+                        const float sv = vis ? s[qb][r + e] : -INFINITY;
+                        pv[e] = fast_exp2(__builtin_fmaf(sv, c, -l4[(r + e) >> 2][(r + e) & 3]));
+                        dsv[e] = pv[e] * (dp[qb][r + e] - d4[(r + e) >> 2][(r + e) & 3]);
+                    }
+                    pp[qb][r >> 1] = E::pack2(pv[0], pv[1]);
+                    dsp[qb][r >> 1] = E::pack2(dsv[0], dsv[1]);
+                }
+            }
+            // dV^T += dout^T P,  dK^T += Q^T dS over the 4 blocks of 16 queries
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                    u32x4_t bp = {pp[qb][4 * cc], pp[qb][4 * cc + 1], pp[qb][4 * cc + 2], pp[qb][4 * cc + 3]};
+                    u32x4_t bs = {dsp[qb][4 * cc], dsp[qb][4 * cc + 1], dsp[qb][4 * cc + 2], dsp[qb][4 * cc + 3]};
+                    const frag fp = __builtin_bit_cast(frag, bp);
+                    const frag fs = __builtin_bit_cast(frag, bs);
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        dv_acc[db] = E::mma(bwd_tr_frag<T, D>(Ov, qb, cc, db, vrow0, vcol0), fp, dv_acc[db]);
+                        dk_acc[db] = E::mma(bwd_tr_frag<T, D>(Qv, qb, cc, db, vrow0, vcol0), fs, dk_acc[db]);
+                    }
+                }
+        }
+        if (it + 1 < ntl) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
+        __syncthreads();
+    };
+    for (int it = 0; it < ntl; it += 2) {
+        tile_step(std::integral_constant<int, 0>{}, it);
+        if (it + 1 < ntl) tile_step(std::integral_constant<int, 1>{}, it + 1);
+    }
+
+    // ---- epilogue: dk = scale * dK^T, dv = dV^T; lane = key column ----
+    if (wave_active && kj < S) {
+        T *rk = dkg + (int64_t)kj * D;
+        T *rv = dvg + (int64_t)kj * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * db + 8 * g4 + 4 * hi;
+                u32x2_t wk = {E::pack2(dk_acc[db][4 * g4] * p.scale, dk_acc[db][4 * g4 + 1] * p.scale),
+                              E::pack2(dk_acc[db][4 * g4 + 2] * p.scale, dk_acc[db][4 * g4 + 3] * p.scale)};
+                u32x2_t wv = {E::pack2(dv_acc[db][4 * g4], dv_acc[db][4 * g4 + 1]),
+                              E::pack2(dv_acc[db][4 * g4 + 2], dv_acc[db][4 * g4 + 3])};
+                *(u32x2_t *)(rk + d) = wk;
+                *(u32x2_t *)(rv + d) = wv;
+            }
+    }
+}
+
+}  // namespace pmkl_amd

@@ -21,6 +21,7 @@
 #include "pmkl_attn.h"
 #include "attn_fwd_kernels.hpp"
 #include "attn_fwd_w64.hpp"
+#include "attn_bwd_kernels.hpp"
 
 namespace {
 
@@ -171,6 +172,37 @@ int check_tensor(const char *name, const void *ptr, const int64_t st[3], int64_t
     return PMKL_OK;
 }
 
+using pmkl_amd::BwdParams;
+typedef void (*bwd_kernel_fn)(BwdParams);
+
+struct BwdKernels {
+    bwd_kernel_fn dq, dkdv;
+    int threads, rows;   // threads and owned rows per workgroup
+};
+
+template <typename T, int D>
+BwdKernels pick_bwd(bool causal) {
+    using TL = pmkl_amd::BwdTile<T, D>;
+    if (causal)
+        return {pmkl_amd::attn_bwd_dq_kernel<T, D, true>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, true>, TL::THREADS,
+                TL::ROWS};
+    return {pmkl_amd::attn_bwd_dq_kernel<T, D, false>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, false>, TL::THREADS,
+            TL::ROWS};
+}
+
+BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
+    if (dt == PMKL_DTYPE_BF16) {
+        if (d == 32) return pick_bwd<__bf16, 32>(causal);
+        if (d == 64) return pick_bwd<__bf16, 64>(causal);
+        if (d == 128) return pick_bwd<__bf16, 128>(causal);
+    } else if (dt == PMKL_DTYPE_F16) {
+        if (d == 32) return pick_bwd<_Float16, 32>(causal);
+        if (d == 64) return pick_bwd<_Float16, 64>(causal);
+        if (d == 128) return pick_bwd<_Float16, 128>(causal);
+    }
+    return {nullptr, nullptr, 0, 0};
+}
+
 }  // namespace
 
 extern "C" {
@@ -268,6 +300,93 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     hipLaunchKernelGGL(kc.fn, dim3((unsigned)grid), dim3(kc.threads), 0, st, p);
     hipError_t err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return PMKL_OK;
+}
+
+uint64_t pmkl_attn_bwd_workspace_size(int64_t batch, int64_t heads, int64_t seq_len) {
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+    return (uint64_t)(2 * batch * heads * seq_len) * sizeof(float);
+}
+
+int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim) {
+    return (dtype == PMKL_DTYPE_F16 || dtype == PMKL_DTYPE_BF16) && head_dim_supported(head_dim) ? 1 : 0;
+}
+
+int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
+    g_err[0] = '\0';
+    PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
+    PMKL_REQUIRE(a->dtype == PMKL_DTYPE_F16 || a->dtype == PMKL_DTYPE_BF16, PMKL_EUNSUPPORTED,
+                 "backward dtype %d has no device kernel (supported: F16, BF16)", (int)a->dtype);
+    PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
+                 "ml_dtype %d must equal dtype %d or be F32", (int)a->ml_dtype, (int)a->dtype);
+    PMKL_REQUIRE(a->batch >= 0 && a->heads >= 0 && a->seq_len >= 0, PMKL_EINVAL,
+                 "negative shape (batch %lld, heads %lld, seq %lld)", (long long)a->batch, (long long)a->heads,
+                 (long long)a->seq_len);
+    PMKL_REQUIRE(head_dim_supported(a->head_dim), PMKL_EUNSUPPORTED,
+                 "head_dim %lld has no compiled kernel (supported: 32, 64, 128)", (long long)a->head_dim);
+    PMKL_REQUIRE(std::isfinite(a->scale) && a->scale >= 0.f, PMKL_EINVAL, "scale must be finite and >= 0");
+    if (a->batch * a->heads * a->seq_len == 0) return PMKL_OK;
+
+    const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
+    PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
+                 (long long)(B * H), (long long)S);
+    PMKL_REQUIRE(B * H * S * D < (1LL << 62), PMKL_EINVAL, "tensors span too many elements");
+    const struct {
+        const char *name;
+        const void *ptr;
+    } tensors[] = {{"dout", a->dout}, {"q", a->q}, {"k", a->k}, {"v", a->v}, {"dq", a->dq}, {"dk", a->dk},
+                   {"dv", a->dv}};
+    for (const auto &t : tensors) {
+        PMKL_REQUIRE(t.ptr != nullptr, PMKL_EINVAL, "%s is a null pointer", t.name);
+        PMKL_REQUIRE(((uintptr_t)t.ptr % 16) == 0, PMKL_EINVAL, "%s must be 16-byte aligned", t.name);
+    }
+    PMKL_REQUIRE(a->o == nullptr || ((uintptr_t)a->o % 16) == 0, PMKL_EINVAL, "o must be 16-byte aligned");
+    PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
+    const size_t ml_es = dtype_size(a->ml_dtype);
+    PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
+                 "m / l must be aligned to their element size");
+    const uint64_t ws = pmkl_attn_bwd_workspace_size(B, H, S);
+    PMKL_REQUIRE(a->workspace != nullptr && ((uintptr_t)a->workspace % 16) == 0, PMKL_EINVAL,
+                 "workspace must be a 16-byte aligned device pointer");
+    PMKL_REQUIRE(a->workspace_bytes >= ws, PMKL_EINVAL, "workspace of %llu bytes is too small (needs %llu)",
+                 (unsigned long long)a->workspace_bytes, (unsigned long long)ws);
+
+    const BwdKernels kc = select_bwd(a->dtype, D, a->is_causal != 0);
+    PMKL_REQUIRE(kc.dq != nullptr, PMKL_EUNSUPPORTED, "no backward kernel for dtype %d head_dim %lld",
+                 (int)a->dtype, (long long)D);
+    const int64_t ntiles = (S + kc.rows - 1) / kc.rows;
+    PMKL_REQUIRE(ntiles * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
+                 (long long)(ntiles * B * H));
+
+    BwdParams p;
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.dout = a->dout;
+    p.m = a->m;
+    p.l = a->l;
+    p.dq = a->dq;
+    p.dk = a->dk;
+    p.dv = a->dv;
+    p.lse2 = (float *)a->workspace;
+    p.drow = (float *)a->workspace + B * H * S;
+    p.S = (int32_t)S;
+    p.BH = (int32_t)(B * H);
+    p.n_qtiles = (int32_t)ntiles;
+    p.n_ktiles = (int32_t)ntiles;
+    p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
+    p.scale_log2 = p.scale * 1.4426950408889634f;
+    p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
+
+    hipStream_t st = (hipStream_t)stream;
+    // dQ first: it writes the row vectors the dK/dV pass reads.
+    hipLaunchKernelGGL(kc.dq, dim3((unsigned)(ntiles * B * H)), dim3(kc.threads), 0, st, p);
+    hipError_t err = hipGetLastError();
+    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dq kernel launch failed: %s", hipGetErrorString(err));
+    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)(ntiles * B * H)), dim3(kc.threads), 0, st, p);
+    err = hipGetLastError();
+    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dk/dv kernel launch failed: %s", hipGetErrorString(err));
     return PMKL_OK;
 }
 

@@ -1,4 +1,4 @@
-"""Autograd entry of the fused self-attention forward.
+"""Autograd entry of the fused self-attention.
 
 Same API as the reference pmkl_pytorch_ext/pmkl_function/__init__.py:1-33:
 ``fused_self_attention(q, k, v, is_casual, debug=False)`` returning
@@ -11,9 +11,11 @@ Dispatch:
   * CPU tensors with debug=True -> the operator's CPU body, as in the
     reference;
   * anything else -> NotImplementedError, as in the reference.
-Backward: the reference computes it only on the CPU with debug=True through
-fused_self_attention_bw (fused_self_attention.cpp:175-215); that operator is
-not part of this forward path, so backward raises NotImplementedError.
+Backward (gradients of out only; those of out_m, out_l are ignored, as in the
+reference, __init__.py:25-32): CPU with debug=True -> fused_self_attention_bw's
+CPU body, as the reference; ROCm fp16 / bf16 tensors -> pmkl_attn_bwd (the
+gfx950 backward), given the saved forward output so its row terms come from
+<dout, out>; anything else -> NotImplementedError.
 """
 import torch
 from torch.autograd import Function
@@ -38,13 +40,25 @@ class fused_self_attention_(Function):
     def setup_context(ctx, inputs, output):
         q, k, v, is_casual, debug = inputs
         out, out_m, out_l = output
-        ctx.save_for_backward(q, k, v, out_m, out_l)
+        ctx.save_for_backward(q, k, v, out, out_m, out_l)
         ctx.is_casual = bool(is_casual)
         ctx.debug = bool(debug)
 
     @staticmethod
     def backward(ctx, grad_output, grad_m, grad_l):
-        raise NotImplementedError("fused_self_attention backward is not implemented by pmkl_amd")
+        q, k, v, out, out_m, out_l = ctx.saved_tensors
+        if q.is_cuda:
+            if q.dtype not in (torch.float16, torch.bfloat16):
+                raise NotImplementedError(f"the device backward supports float16 and bfloat16, got {q.dtype}")
+            from .. import attn_bwd
+
+            dq, dk, dv = attn_bwd(grad_output.contiguous(), q.contiguous(), k.contiguous(), v.contiguous(),
+                                  out_m, out_l, is_causal=ctx.is_casual, out=out)
+        elif q.is_cpu and ctx.debug:
+            dq, dk, dv = pmkl_pytorch_ext.fused_self_attention_bw(grad_output, q, k, v, out_m, out_l, ctx.is_casual)
+        else:
+            raise NotImplementedError()
+        return dq, dk, dv, None, None
 
 
 fused_self_attention = fused_self_attention_.apply

@@ -1,0 +1,175 @@
+"""GPU parity tests of the gfx950 attention backward (pmkl_attn_bwd through the
+C ABI), against the float64 backward oracle (oracle_attn_bwd, the restatement
+of pmkl_pytorch_ext/fused_self_attention.cpp:66-135).
+
+The device forward runs first and its m, l (in the tensor dtype, as the
+reference's autograd saves them) feed both the device backward and the
+oracle, so both use the same probabilities P = exp(s - m) / l.
+
+Tolerance: the kernels round P and dS to the tensor dtype for the MFMA
+products and round dq, dk, dv on output; accumulation is fp32.  Each
+gradient tensor is held to max|g - g_ref| <= TOL * max|g_ref| (+ the half-ulp
+output rounding of each element), TOL = 1.5e-2 for bf16 and 3e-3 for fp16.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": 1.5e-2, "fp16": 3e-3}
+MANT = {"bf16": 7, "fp16": 10}
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _np(t):
+    import torch
+
+    return t.detach().to("cpu", torch.float32).numpy().astype(np.float64)
+
+
+def _run(B, H, S, D, dtype, causal, seed, with_o=False, dist="normal", heads=None):
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd.workloads import small_inputs, torch_dtype
+
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=seed, dist=dist)
+    rng = np.random.Generator(np.random.PCG64(seed + 17))
+    do = torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to(torch_dtype(dtype))
+    qd, kd, vd, dod = (x.to("cuda:0") for x in (q, k, v, do))
+    o, m, l = pmkl_amd.attn_fwd(qd, kd, vd, is_causal=causal)
+    dq, dk, dv = pmkl_amd.attn_bwd(dod, qd, kd, vd, m, l, is_causal=causal, out=o if with_o else None)
+    torch.cuda.synchronize()
+    r = lambda t: _np(t).reshape(B * H, S, D)
+    ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), _np(m).reshape(B * H, S), _np(l).reshape(B * H, S),
+                          causal=causal, heads=heads)
+    got = [r(x) if heads is None else r(x)[list(heads)] for x in (dq, dk, dv)]
+    return got, ref
+
+
+def _check(got, ref, dtype, label):
+    errs = {}
+    for name, g, w in zip(("dq", "dk", "dv"), got, ref):
+        assert np.isfinite(g).all(), f"{label}: {name} not finite"
+        scale = max(float(np.abs(w).max()), 1e-30)
+        bound = TOL[dtype] * scale + oracle.ulp(w, MANT[dtype]) / 2
+        err = np.abs(g - w)
+        worst = float((err / bound).max())
+        errs[name] = (float(err.max()) / scale, worst)
+        assert worst <= 1.0, f"{label}: {name} beyond bound (max rel err {err.max() / scale:.3g}, worst {worst:.3f})"
+    return errs
+
+
+SHAPES = [
+    (1, 1, 1, "S=1"),
+    (1, 2, 33, "ragged"),
+    (2, 1, 64, "one tile"),
+    (1, 2, 100, "ragged multi"),
+    (1, 1, 256, "one workgroup"),
+    (2, 2, 300, "two workgroups, ragged"),
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_bwd_small_shapes_vs_oracle(device, dtype, D, causal):
+    for i, (B, H, S, label) in enumerate(SHAPES):
+        tag = f"bwd {dtype} D={D} causal={causal} B{B} H{H} S{S} ({label})"
+        _say(f"case {tag}")
+        got, ref = _run(B, H, S, D, dtype, causal, seed=300 + i)
+        errs = _check(got, ref, dtype, tag)
+        _say(f"  {errs}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_bwd_with_forward_output(device, dtype):
+    """Row terms from <dout, O> instead of the extra pass over the keys."""
+    for causal in (True, False):
+        tag = f"bwd with O {dtype} causal={causal}"
+        _say(f"case {tag}")
+        got, ref = _run(2, 2, 300, 64, dtype, causal, seed=400, with_o=True)
+        _check(got, ref, dtype, tag)
+
+
+def test_bwd_larger_heads_sampled(device):
+    """S = 1024, head_dim 128, bf16: two heads against the oracle."""
+    tag = "bwd bf16 B1 H4 S1024 D128"
+    _say(f"case {tag}")
+    got, ref = _run(1, 4, 1024, 128, "bf16", True, seed=500, heads=[0, 3])
+    _check(got, ref, "bf16", tag)
+
+
+def test_bwd_closed_form_constant_v(device):
+    """Constant V: O does not depend on q, k, so dq = dk = 0.  With m, l in
+    float32 the probabilities of a row sum to 1 within float32 rounding, so
+    dS = P (dP - sum P dP) vanishes up to that (with m, l rounded to bf16 the
+    row sums are off by up to 2^-9 and dq, dk are small but not zero, in the
+    reference's algorithm as well)."""
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd.workloads import small_inputs
+
+    q, k, _ = small_inputs(1, 2, 200, 64, "bf16", seed=9)
+    v = torch.full_like(q, 0.5)
+    do = torch.ones_like(q)
+    qd, kd, vd, dod = (x.to("cuda:0") for x in (q, k, v, do))
+    o, m, l = pmkl_amd.attn_fwd(qd, kd, vd, is_causal=True, ml_dtype=torch.float32)
+    dq, dk, dv = pmkl_amd.attn_bwd(dod, qd, kd, vd, m, l, is_causal=True)
+    torch.cuda.synchronize()
+    assert float(dq.abs().max()) <= 1e-2 and float(dk.abs().max()) <= 1e-2
+    # dv_j = sum_{i >= j} P_ij: the column sums of P; the total over j is S per head
+    tot = dv.float().sum(dim=2)[..., 0]
+    assert torch.allclose(tot.cpu(), torch.full_like(tot.cpu(), 200.0), rtol=2e-2)
+
+
+def test_bwd_error_paths(device):
+    import torch
+
+    import pmkl_amd
+
+    q = torch.zeros((1, 1, 64, 64), dtype=torch.float32, device="cuda:0")
+    m = torch.zeros((1, 1, 64), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(Exception, match="dtype"):
+        pmkl_amd.attn_bwd(q, q, q, q, m, m)
+
+
+def test_bwd_torch_operator_and_autograd_device(device):
+    """fused_self_attention_bw on ROCm tensors runs the device backward (same
+    result as the C ABI call); the autograd entry's device branch, which hands
+    the saved forward output to the kernel, is within the bound of the oracle."""
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd import pmkl_pytorch_ext
+    from pmkl_amd.pmkl_function import fused_self_attention
+    from pmkl_amd.workloads import small_inputs
+
+    B, H, S, D = 1, 2, 300, 64
+    q, k, v = small_inputs(B, H, S, D, "bf16", seed=600)
+    do = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(601)).to(torch.bfloat16)
+    qd, kd, vd, dod = (x.to("cuda:0") for x in (q, k, v, do))
+    o, m, l = pmkl_pytorch_ext.fused_self_attention_fw(qd, kd, vd, True)
+    a = pmkl_pytorch_ext.fused_self_attention_bw(dod, qd, kd, vd, m, l, True)
+    b = pmkl_amd.attn_bwd(dod, qd, kd, vd, m, l, is_causal=True)
+    torch.cuda.synchronize()
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (qd, kd, vd))
+    out, mm, ll = fused_self_attention(qg, kg, vg, True)
+    out.backward(dod)
+    torch.cuda.synchronize()
+    r = lambda t: _np(t).reshape(B * H, S, D)
+    ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), _np(mm).reshape(B * H, S), _np(ll).reshape(B * H, S), causal=True)
+    _check([r(qg.grad), r(kg.grad), r(vg.grad)], ref, "bf16", "autograd device")

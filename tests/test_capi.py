@@ -37,7 +37,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_abi_version_and_support_matrix():
     lib = capi.load()
-    assert lib.pmkl_abi_version() == 1
+    assert lib.pmkl_abi_version() == 2
     for dt in (capi.PMKL_DTYPE_F32, capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
         for d in (32, 64, 128):
             assert lib.pmkl_attn_fwd_supported(dt, d) == 1
@@ -120,3 +120,47 @@ def test_args_struct_layout_matches_header(tmp_path):
     for f in fields:
         assert int(out[f]) == getattr(capi.AttnFwdArgs, f).offset, f
     assert int(out["sizeof"]) == ctypes.sizeof(capi.AttnFwdArgs)
+
+
+def _bwd_args(**kw):
+    base = dict(dout=0x1000, q=0x2000, k=0x3000, v=0x4000, o=0, m=0x5000, l=0x6000, dq=0x7000, dk=0x8000,
+                dv=0x9000, workspace=0xa000, workspace_bytes=1 << 20, dtype=capi.PMKL_DTYPE_BF16,
+                batch=1, heads=2, seq_len=64, head_dim=64)
+    base.update(kw)
+    return capi.make_bwd_args(**base)
+
+
+def _expect_bwd(args, code, pattern):
+    rc = capi.attn_bwd_raw(args)
+    msg = capi.last_error()
+    assert rc == code, (rc, msg)
+    assert re.search(pattern, msg), msg
+    assert re.search(r"pmkl check failed at attn_capi\.hip:\d+", msg), msg
+
+
+def test_bwd_workspace_size_and_support():
+    lib = capi.load()
+    assert lib.pmkl_attn_bwd_workspace_size(4, 32, 4096) == 2 * 4 * 32 * 4096 * 4
+    assert lib.pmkl_attn_bwd_workspace_size(0, 32, 4096) == 0
+    for dt in (capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
+        for d in (32, 64, 128):
+            assert lib.pmkl_attn_bwd_supported(dt, d) == 1
+        assert lib.pmkl_attn_bwd_supported(dt, 80) == 0
+    assert lib.pmkl_attn_bwd_supported(capi.PMKL_DTYPE_F32, 64) == 0
+
+
+def test_bwd_error_paths():
+    lib = capi.load()
+    assert lib.pmkl_attn_bwd(None, None) == capi.PMKL_EINVAL
+    _expect_bwd(_bwd_args(dtype=capi.PMKL_DTYPE_F32), capi.PMKL_EUNSUPPORTED, "no device kernel")
+    _expect_bwd(_bwd_args(ml_dtype=capi.PMKL_DTYPE_F16), capi.PMKL_EINVAL, "ml_dtype")
+    _expect_bwd(_bwd_args(seq_len=-1), capi.PMKL_EINVAL, "negative shape")
+    _expect_bwd(_bwd_args(head_dim=96), capi.PMKL_EUNSUPPORTED, "head_dim 96")
+    _expect_bwd(_bwd_args(dq=0), capi.PMKL_EINVAL, "dq is a null pointer")
+    _expect_bwd(_bwd_args(k=0x3008), capi.PMKL_EINVAL, "k must be 16-byte aligned")
+    _expect_bwd(_bwd_args(o=0x3008), capi.PMKL_EINVAL, "o must be 16-byte aligned")
+    _expect_bwd(_bwd_args(l=0), capi.PMKL_EINVAL, "m / l must not be null")
+    _expect_bwd(_bwd_args(workspace=0), capi.PMKL_EINVAL, "workspace must be")
+    _expect_bwd(_bwd_args(workspace_bytes=100), capi.PMKL_EINVAL, "workspace of 100 bytes is too small")
+    # an empty problem succeeds without touching anything
+    assert capi.attn_bwd_raw(_bwd_args(seq_len=0, dq=0, workspace=0)) == capi.PMKL_OK

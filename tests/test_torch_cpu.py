@@ -7,7 +7,9 @@ reference dispatches (float, double, half, bfloat16).  This is checked against
 the committed fixtures (outputs of the reference operator built from its
 source) and, where oracle/_ref is built, live on fresh inputs.  The
 pmkl_function wrapper keeps the reference's API and CPU/debug behaviour
-(pmkl_function/__init__.py:12-33).
+(pmkl_function/__init__.py:12-33).  fused_self_attention_bw's CPU body is held
+to the reference's backward operator (fused_self_attention.cpp:66-135) the
+same way, through tests/golden/bwd_*.npz.
 """
 from __future__ import annotations
 
@@ -95,7 +97,54 @@ def test_pmkl_function_cpu_debug_and_errors():
     assert all(torch.equal(a, b) for a, b in zip(out, ref))
     with pytest.raises(NotImplementedError):
         fused_self_attention(q, k, v, True)          # CPU without debug, as in the reference
-    qg = q.clone().requires_grad_(True)
-    o, _, _ = fused_self_attention(qg, k, v, True, True)
-    with pytest.raises(NotImplementedError):
-        o.sum().backward()
+    # backward on the CPU with debug: the operator's CPU body, as in the reference
+    qg, kg, vg = (x.clone().requires_grad_(True) for x in (q, k, v))
+    o, m, l = fused_self_attention(qg, kg, vg, True, True)
+    gout = torch.randn(o.shape, generator=g)
+    o.backward(gout)
+    want = pmkl_pytorch_ext.fused_self_attention_bw(gout, q, k, v, m.detach(), l.detach(), True)
+    for got, w in zip((qg.grad, kg.grad, vg.grad), want):
+        assert torch.equal(got, w)
+
+
+BWD_FIXTURES = sorted(GOLDEN.glob("bwd_*.npz"))
+
+
+@pytest.mark.parametrize("dt", list(TORCH))
+@pytest.mark.parametrize("path", BWD_FIXTURES, ids=lambda p: p.stem)
+def test_cpu_backward_bit_exact_vs_reference_fixture(path, dt):
+    """fused_self_attention_bw's CPU body == the reference operator's, bit for bit
+    (fused_self_attention.cpp:66-135,175-215), on the m, l its forward returned."""
+    with np.load(path, allow_pickle=False) as z:
+        f = {k: z[k] for k in z.files}
+    B, H, S, D, causal = int(f["B"]), int(f["H"]), int(f["S"]), int(f["D"]), bool(f["causal"])
+    q, k, v, do = (torch.from_numpy(f[x]).reshape(B, H, S, D).to(TORCH[dt]) for x in ("q", "k", "v", "dout"))
+    m = _stored(f[f"m_{dt}"], dt).reshape(B, H, S)
+    l = _stored(f[f"l_{dt}"], dt).reshape(B, H, S)
+    dq, dk, dv = pmkl_pytorch_ext.fused_self_attention_bw(do, q, k, v, m, l, causal)
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        assert got.dtype == TORCH[dt]
+        assert torch.equal(got, _stored(f[f"{name}_{dt}"], dt).reshape(B, H, S, D)), (name, dt)
+
+
+def test_cpu_backward_bit_exact_vs_reference_build_live():
+    ref = oracle.reference_op()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (the reference tree is absent)")
+    g = torch.Generator().manual_seed(6)
+    for dt in TORCH.values():
+        for (B, H, S, D, causal) in [(1, 2, 19, 32, True), (1, 1, 24, 64, False)]:
+            q, k, v, do = (torch.randn(B, H, S, D, generator=g).to(dt) for _ in range(4))
+            _, m, l = ref.fused_self_attention_fw(q, k, v, causal)
+            a = pmkl_pytorch_ext.fused_self_attention_bw(do, q, k, v, m, l, causal)
+            b = ref.fused_self_attention_bw(do, q, k, v, m, l, causal)
+            assert all(torch.equal(x, y) for x, y in zip(a, b)), (dt, B, H, S, D, causal)
+
+
+def test_backward_checks_match_reference_messages():
+    x = torch.randn(1, 2, 8, 32)
+    m = torch.randn(1, 2, 8)
+    with pytest.raises(RuntimeError, match="Input tensor must be contiguous"):
+        pmkl_pytorch_ext.fused_self_attention_bw(x, x.transpose(2, 3), x, x, m, m, True)
+    with pytest.raises(RuntimeError, match="Input tensor shapes must match"):
+        pmkl_pytorch_ext.fused_self_attention_bw(x, x, x[:, :1].contiguous(), x, m, m, True)
