@@ -57,6 +57,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--op", default="fwd", choices=["fwd", "bwd"],
+                    help="fwd: the headline forward (default); bwd: the backward (pmkl_attn_bwd), "
+                         "its own JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 512 MiB device copy (torch copy kernel) so that rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
@@ -119,6 +122,81 @@ def cpu_baseline(w):
     }
 
 
+def bench_bwd(args):
+    """Backward of the attention output (pmkl_attn_bwd) on the workload: one
+    step is one call (two kernel launches), inputs resident in HBM.  FLOPs:
+    10*D per visible (i, j) pair (the five products QK^T, dout V^T, P^T dout,
+    dS^T Q, dS K), i.e. 2.5x the forward's count; the pass that forms
+    sum_j P dP from the keys when O is not given is not counted."""
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd import capi
+    from pmkl_amd.workloads import WORKLOADS, causal_flops, torch_inputs
+
+    w = WORKLOADS[args.config]
+    if w.dtype == "fp32":
+        raise SystemExit("bench.py --op bwd: the device backward runs fp16 / bf16 only")
+    dev = torch.device("cuda:0")
+    q, k, v = torch_inputs(w, dev)
+    g = torch.Generator(device="cpu").manual_seed(w.seed + 1)
+    do = torch.randn(q.shape, generator=g).to(q.dtype).to(dev)
+    o, m, l = pmkl_amd.attn_fwd(q, k, v, is_causal=True)
+    dq, dk, dv = (torch.empty_like(x) for x in (q, k, v))
+    lib = capi.load()
+    ws_bytes = int(lib.pmkl_attn_bwd_workspace_size(w.B, w.H, w.S))
+    ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    dt = pmkl_amd.torch_dtype_to_pmkl(q.dtype)
+    results = {}
+    for with_o in (False, True):
+        cargs = capi.make_bwd_args(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   o.data_ptr() if with_o else 0, m.data_ptr(), l.data_ptr(), dq.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, dtype=dt, batch=w.B,
+                                   heads=w.H, seq_len=w.S, head_dim=w.D, is_causal=True)
+
+        def step():
+            rc = capi.attn_bwd_raw(cargs, stream.cuda_stream)
+            if rc != capi.PMKL_OK:
+                raise capi.PmklError(rc, capi.last_error())
+
+        t_w = time.perf_counter()
+        while time.perf_counter() - t_w < WARMUP_MIN_S:
+            for _ in range(max(args.warmup, 1)):
+                step()
+            torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for _ in range(args.steps):
+            step()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        results[with_o] = ev0.elapsed_time(ev1) / args.steps
+    flops = causal_flops(w.B, w.H, w.S, w.D) * 10 // 4
+    peak = PEAK_TFLOPS[w.dtype]
+    ms = results[False]
+    line = {
+        "metric": f"causal-attn backward TFLOP/s on 1 MI355X, {w.dtype} B{w.B} H{w.H} S{w.S} D{w.D}",
+        "value": round(flops / (ms / 1e3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "dtype": w.dtype,
+        "data": "synthetic: seeded PCG64 " + w.note + "; dout ~ N(0,1)",
+        "config": {"workload": f"{w.name} causal self-attention bwd {w.dtype} B{w.B} H{w.H} S{w.S} D{w.D}",
+                   "flops_per_step": flops, "flop_count": "10*D per visible pair (5 products)"},
+        "pct_of_mfma_peak": round(100.0 * flops / (ms / 1e3) / 1e12 / peak, 2),
+        "with_o": {"ms_per_step": round(results[True], 4),
+                   "value": round(flops / (results[True] / 1e3) / 1e12, 2)},
+        "kernels": ["attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"],
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -128,6 +206,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.op == "bwd":
+        bench_bwd(args)
         return
 
     import torch
