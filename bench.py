@@ -57,7 +57,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--op", default="fwd", choices=["fwd", "bwd"],
+    ap.add_argument("--op", default="fwd", choices=["fwd", "bwd", "softmax"],
                     help="fwd: the headline forward (default); bwd: the backward (pmkl_attn_bwd), "
                          "its own JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -79,10 +79,11 @@ def calibrate_copy():
     print(json.dumps({"calibration": "copy", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}))
 
 
-def read_traffic(config: str, kernel: str):
-    """HBM bytes per launch from profiles/pmc_attn_fwd_<config>.txt when that
-    summary was measured on `kernel` (its "kernel_id:" line), else None."""
-    path = ROOT / "profiles" / f"pmc_attn_fwd_{config}.txt"
+def read_traffic(config: str, kernel: str, name: str | None = None):
+    """HBM bytes per launch from profiles/pmc_attn_fwd_<config>.txt (or
+    profiles/<name>) when that summary was measured on `kernel` (its
+    "kernel_id:" line), else None."""
+    path = ROOT / "profiles" / (name or f"pmc_attn_fwd_{config}.txt")
     if not path.exists():
         return None
     txt = path.read_text()
@@ -197,6 +198,88 @@ def bench_bwd(args):
     print(json.dumps(line), flush=True)
 
 
+SOFTMAX_ROWS, SOFTMAX_N = 131072, 1024
+
+
+def bench_softmax(args):
+    """Row softmax (pmkl_softmax_fwd, the replacement of
+    pmkl::norm::warp_softmax_forward) over 131,072 rows x 1,024 fp32 elements:
+    the score rows of C2 (B*H*S = 8*16*1024 rows of S = 1024 keys) at the
+    reference's widest row and its tested dtype.  A step is one call (one
+    launch), inputs resident in HBM.  Algorithmic bytes per call: every
+    element read once and written once, rows * n * (4 + 4) = 1 GiB."""
+    import torch
+
+    from pmkl_amd import capi
+
+    rows, n = SOFTMAX_ROWS, SOFTMAX_N
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1006)
+    x = torch.rand((rows, n), generator=g, device=dev) * 20.0 - 10.0
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream(dev)
+    handle = stream.cuda_stream
+    cargs = capi.make_softmax_args(y.data_ptr(), x.data_ptr(), out_dtype=capi.PMKL_DTYPE_F32,
+                                   in_dtype=capi.PMKL_DTYPE_F32, elements=n, stride=n, batch=rows)
+
+    def step():
+        rc = capi.softmax_raw(cargs, handle)
+        if rc != capi.PMKL_OK:
+            raise capi.PmklError(rc, capi.last_error())
+
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < WARMUP_MIN_S:
+        for _ in range(max(args.warmup, 1)):
+            step()
+        torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    avg_ms = ev0.elapsed_time(ev1) / args.steps
+    alg_bytes = rows * n * (4 + 4)
+    achieved = alg_bytes / (avg_ms / 1e3) / 1e9
+    kernel = "softmax_fwd_kernel<float, float, 4, 4, false>"
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle
+
+        xh = x.cpu().numpy()
+        t0 = time.perf_counter()
+        oracle.softmax_host_f32(xh)
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(alg_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"the whole workload ({rows} x {n} fp32) through the reference's CPU softmax check "
+                         f"host_softmax_forward (test/test_softmax.cpp:10-28) restated in C, single-threaded; "
+                         f"{cpu_s:.2f} s"}
+    line = {
+        "metric": f"row softmax GB/s on 1 MI355X, fp32 {rows} rows x {n}",
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(avg_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: U(-10, 10) from torch's seeded device generator (seed 1006)",
+        "config": {"workload": f"row softmax fp32 rows={rows} n={n} stride={n}", "rows": rows, "elements": n,
+                   "alg_bytes_per_step": alg_bytes, "byte_count": "rows*n*(4 read + 4 written)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": read_traffic("", kernel, "pmc_softmax_fwd_fp32_131072x1024.txt"),
+                     "kernel": kernel, "avg_launch_us": round(avg_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -209,6 +292,9 @@ def main():
         return
     if args.op == "bwd":
         bench_bwd(args)
+        return
+    if args.op == "softmax":
+        bench_softmax(args)
         return
 
     import torch

@@ -13,7 +13,7 @@
 // What changes: the work runs in the gfx950 kernels behind pmkl_attn.h, on
 // pmkl::current_stream(); scalar_t may be float or a 16-bit type
 // (pmkl::half_t / _Float16, pmkl::bfloat16_t / __bf16; other 16-bit types
-// can specialise pmkl::attn_dtype); HIDDEN_SIZE may be 32, 64 or 128; launch
+// can specialise pmkl::dtype_code, pmkl/dtype.h); HIDDEN_SIZE may be 32, 64 or 128; launch
 // errors are reported.  BLOCK_M is validated as in the reference but the tile
 // shape is the kernel's own.
 #pragma once
@@ -22,43 +22,9 @@
 
 #include "../../pmkl_attn.h"
 #include "../core.h"
+#include "../dtype.h"
 
 namespace pmkl {
-
-// 16-bit storage types for host code that has no native half/bfloat16 type.
-struct half_t {
-    uint16_t bits;
-};
-struct bfloat16_t {
-    uint16_t bits;
-};
-
-template <typename T>
-struct attn_dtype {
-    static constexpr int value = -1;
-};
-template <>
-struct attn_dtype<float> {
-    static constexpr int value = PMKL_DTYPE_F32;
-};
-template <>
-struct attn_dtype<half_t> {
-    static constexpr int value = PMKL_DTYPE_F16;
-};
-template <>
-struct attn_dtype<bfloat16_t> {
-    static constexpr int value = PMKL_DTYPE_BF16;
-};
-#if defined(__clang__)
-template <>
-struct attn_dtype<_Float16> {
-    static constexpr int value = PMKL_DTYPE_F16;
-};
-template <>
-struct attn_dtype<__bf16> {
-    static constexpr int value = PMKL_DTYPE_BF16;
-};
-#endif
 namespace nlp {
 
 template <typename scalar_t, int BLOCK_M = 32, int HIDDEN_SIZE = 64>
@@ -66,7 +32,7 @@ void causal_attention_forward(scalar_t *out, const scalar_t *q, const scalar_t *
                               const int batch_size, const int num_heads, const int seq_length, scalar_t *out_m,
                               scalar_t *out_l) {
     constexpr int WARP_SIZE = 32;  // the reference's row-tile contract, not the hardware wave size
-    static_assert(attn_dtype<scalar_t>::value >= 0, "scalar_t must be float or a 16-bit float type");
+    static_assert(dtype_code<scalar_t>::value >= 0, "scalar_t must be float or a 16-bit float type");
     static_assert(HIDDEN_SIZE == 32 || HIDDEN_SIZE == 64 || HIDDEN_SIZE == 128,
                   "HIDDEN_SIZE must be 32, 64 or 128");
     CHECK_FAIL(seq_length % BLOCK_M == 0);
@@ -75,7 +41,7 @@ void causal_attention_forward(scalar_t *out, const scalar_t *q, const scalar_t *
     if (batch_size * num_heads * seq_length == 0) return;
 
     hipStream_t stream = current_stream();
-    const int rc = pmkl_causal_attention_forward(attn_dtype<scalar_t>::value, out, q, k, v, batch_size, num_heads,
+    const int rc = pmkl_causal_attention_forward(dtype_code<scalar_t>::value, out, q, k, v, batch_size, num_heads,
                                                  seq_length, HIDDEN_SIZE, out_m, out_l, (void *)stream);
     CHECK_FAIL(rc == PMKL_OK, pmkl_last_error());
     PMKL_HIP_CHECK(hipStreamSynchronize(stream));

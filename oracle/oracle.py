@@ -9,6 +9,11 @@ include/) never imports it.
   (pmkl_pytorch_ext/fused_self_attention.cpp:5-64); see attn_oracle.c.
 * ``attn_bwd`` - the float64 restatement of the reference's backward
   operator (fused_self_attention.cpp:66-135), gradients of O only.
+* ``softmax_f64`` - the float64 restatement of the reference row softmax /
+  log-softmax (pmkl/norm/warp_softmax.h:74-201); see softmax_oracle.c.
+* ``softmax_host_f32`` - the reference's CPU check of that softmax
+  (test/test_softmax.cpp:10-28) op for op in float: the benchmark's CPU
+  baseline.
 * ``reference_op`` - the reference's own CPU operator compiled from its source
   into oracle/_ref (oracle/Makefile), or None when that build is absent.
 * ``attn_sdpa_f64`` - torch.nn.functional.scaled_dot_product_attention in
@@ -48,6 +53,10 @@ def _lib():
                                         ctypes.c_int, ctypes.c_double, ctypes.POINTER(ctypes.c_int64),
                                         ctypes.c_int64, dp, dp, dp]
         lib.oracle_attn_bwd.restype = ctypes.c_int
+        lib.oracle_softmax_f64.argtypes = [dp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, dp]
+        lib.oracle_softmax_f64.restype = ctypes.c_int
+        lib.oracle_softmax_host_f32.argtypes = [fp, fp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.oracle_softmax_host_f32.restype = None
         _LIB = lib
     return _LIB
 
@@ -121,6 +130,35 @@ def attn_bwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, dout: np.ndarray, m: n
     return tuple(out)
 
 
+def softmax_f64(x: np.ndarray, n: int | None = None, is_log: bool = False) -> np.ndarray:
+    """Float64 row softmax oracle.  x: [batch, stride] (any float dtype, taken
+    exactly as float64); the first n columns of each row (default: all) are
+    the row.  Returns [batch, n] float64."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float64))
+    if x.ndim == 1:
+        x = x[None, :]
+    assert x.ndim == 2
+    batch, stride = x.shape
+    n = stride if n is None else n
+    y = np.full((batch, stride), np.nan, dtype=np.float64)
+    dp = ctypes.POINTER(ctypes.c_double)
+    if _lib().oracle_softmax_f64(x.ctypes.data_as(dp), n, stride, batch, 1 if is_log else 0, y.ctypes.data_as(dp)):
+        raise RuntimeError("oracle_softmax_f64 failed")
+    return y[:, :n]
+
+
+def softmax_host_f32(x: np.ndarray, n: int | None = None) -> np.ndarray:
+    """The reference's CPU softmax check (test/test_softmax.cpp:10-28) in float.
+    x: float32 [batch, stride]; returns [batch, n] float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    batch, stride = x.shape
+    n = stride if n is None else n
+    y = np.zeros_like(x)
+    fp = ctypes.POINTER(ctypes.c_float)
+    _lib().oracle_softmax_host_f32(y.ctypes.data_as(fp), x.ctypes.data_as(fp), n, stride, batch)
+    return y[:, :n]
+
+
 def reference_op():
     """The reference operator module built into oracle/_ref, or None."""
     global _REF
@@ -167,4 +205,4 @@ def ulp(x: np.ndarray, mant_bits: int) -> np.ndarray:
     return np.ldexp(1.0, (e - mant_bits).astype(np.int64))
 
 
-__all__ = ["attn_fwd_rows", "attn_bwd", "default_scale", "reference_op", "attn_sdpa_f64", "causal_flops", "ulp"]
+__all__ = ["attn_fwd_rows", "attn_bwd", "softmax_f64", "softmax_host_f32", "default_scale", "reference_op", "attn_sdpa_f64", "causal_flops", "ulp"]

@@ -3,17 +3,21 @@
 Drop-in replacement for pmkl's attention path:
   * C++:    include/pmkl/nlp/causal_attention.h  (pmkl::nlp::causal_attention_forward)
   * C ABI:  include/pmkl_attn.h                  (libpmkl_attn.so)
-  * torch:  pmkl_amd.pmkl_pytorch_ext.fused_self_attention_fw
+  * torch:  pmkl_amd.pmkl_pytorch_ext.fused_self_attention_fw / _bw
   * Python: pmkl_amd.pmkl_function.fused_self_attention
+and for the row softmax the fused kernel replaces:
+  * C++:    include/pmkl/norm/warp_softmax.h     (pmkl::norm::warp_softmax_forward)
+  * C ABI:  include/pmkl_softmax.h               (libpmkl_attn.so)
 
-`attn_fwd` below calls the C ABI directly on device tensors through ctypes;
-it is what the parity tests and the benchmark use.
+`attn_fwd`, `attn_bwd`, `warp_softmax_forward` and `softmax` below call the C
+ABI directly on device tensors through ctypes; they are what the parity tests
+and the benchmark use.
 """
 from __future__ import annotations
 
 from . import capi
 
-__all__ = ["attn_fwd", "attn_bwd", "capi", "torch_dtype_to_pmkl"]
+__all__ = ["attn_fwd", "attn_bwd", "warp_softmax_forward", "softmax", "capi", "torch_dtype_to_pmkl"]
 
 
 def torch_dtype_to_pmkl(dt) -> int:
@@ -109,3 +113,58 @@ def attn_bwd(dout, q, k, v, out_m, out_l, is_causal: bool = True, scale: float |
     if rc != capi.PMKL_OK:
         raise capi.PmklError(rc, capi.last_error())
     return dq, dk, dv
+
+
+def warp_softmax_forward(dst, src, softmax_elements: int, softmax_elements_stride: int, batch_count: int,
+                         is_log_softmax: bool = False, stream=None) -> None:
+    """pmkl::norm::warp_softmax_forward (pmkl/norm/warp_softmax.h:159-201) on
+    ROCm tensors: row r of `src` (elements [r*stride, r*stride + n)) goes to
+    the same place in `dst`.  The dtypes of dst and src (float32, float16,
+    bfloat16) play the template's output_t and input_t; accumulation is fp32.
+    Asynchronous on `stream` or torch's current stream."""
+    import torch
+
+    for name, t in (("dst", dst), ("src", src)):
+        if not t.is_cuda:
+            raise ValueError(f"warp_softmax_forward takes ROCm device tensors ({name} is not)")
+    need = 0 if batch_count <= 0 or softmax_elements <= 0 else \
+        (batch_count - 1) * softmax_elements_stride + softmax_elements
+    for name, t in (("dst", dst), ("src", src)):
+        if t.numel() < need or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous tensor of at least {need} elements")
+    if stream is None:
+        stream = torch.cuda.current_stream(src.device).cuda_stream
+    a = capi.make_softmax_args(dst.data_ptr(), src.data_ptr(), out_dtype=torch_dtype_to_pmkl(dst.dtype),
+                               in_dtype=torch_dtype_to_pmkl(src.dtype), elements=softmax_elements,
+                               stride=softmax_elements_stride, batch=batch_count, is_log=is_log_softmax)
+    rc = capi.softmax_raw(a, stream)
+    if rc != capi.PMKL_OK:
+        raise capi.PmklError(rc, capi.last_error())
+
+
+def softmax(x, is_log: bool = False, out_dtype=None, stream=None):
+    """Softmax (or log-softmax) over the last dimension (<= 1024 elements) of
+    a ROCm tensor, through pmkl_softmax_fwd.  Rows must be evenly strided with
+    the last dimension contiguous (anything else is copied first); the result
+    has x's shape, in out_dtype (default x.dtype), with the same row stride."""
+    import torch
+
+    if not x.is_cuda:
+        raise ValueError("softmax takes a ROCm device tensor")
+    n = x.shape[-1] if x.dim() else 1
+    x2 = x.reshape(-1, n)
+    if x2.numel() and (x2.stride(1) != 1 or x2.stride(0) < n):
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    stride = x2.stride(0) if rows > 1 else n
+    out_full = torch.empty((rows, max(stride, n)), dtype=out_dtype or x.dtype, device=x.device)
+    out = out_full[:, :n]
+    if stream is None:
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+    a = capi.make_softmax_args(out_full.data_ptr(), x2.data_ptr(), out_dtype=torch_dtype_to_pmkl(out.dtype),
+                               in_dtype=torch_dtype_to_pmkl(x.dtype), elements=n, stride=stride, batch=rows,
+                               is_log=is_log)
+    rc = capi.softmax_raw(a, stream)
+    if rc != capi.PMKL_OK:
+        raise capi.PmklError(rc, capi.last_error())
+    return out.view(x.shape)

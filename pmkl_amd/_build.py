@@ -1,7 +1,8 @@
 """In-tree build of the native parts of pmkl_amd.
 
 Products (all next to their sources, so they travel with the tree):
-  pmkl_amd/libpmkl_attn.so                 gfx950 kernels + C ABI (hipcc)
+  pmkl_amd/libpmkl_attn.so                 gfx950 kernels + C ABI (hipcc): attention
+                                           forward/backward and row softmax
   pmkl_amd/pmkl_pytorch_ext.<ext-suffix>   torch operator over the C ABI (g++)
 
 Every function compiles unconditionally; nothing is skipped because an output
@@ -45,11 +46,29 @@ def _run(cmd: list[str], cwd: Path = ROOT) -> None:
         raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{err}")
 
 
+CAPI_SOURCES = ("attn_capi.hip", "softmax_capi.hip")
+
+
 def build_capi() -> Path:
-    tmp = CAPI_LIB.with_suffix(".so.tmp")
-    _run([HIPCC, *HIP_FLAGS, "-shared", "-I", str(INCLUDE),
-          str(CSRC / "attn_capi.hip"), "-o", str(tmp)])
-    os.replace(tmp, CAPI_LIB)
+    """Compiles each C ABI source to an object in parallel, then links them."""
+    objs = [CAPI_LIB.parent / (Path(src).stem + ".o.tmp") for src in CAPI_SOURCES]
+    procs = [subprocess.Popen([HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-c", str(CSRC / src), "-o", str(obj)],
+                              cwd=str(ROOT), stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+             for src, obj in zip(CAPI_SOURCES, objs)]
+    errors = []
+    for src, proc in zip(CAPI_SOURCES, procs):
+        out, err = proc.communicate()
+        if proc.returncode != 0:
+            errors.append(f"{src} ({proc.returncode}):\n{out}\n{err}")
+    try:
+        if errors:
+            raise RuntimeError("build step failed: " + "\n".join(errors))
+        tmp = CAPI_LIB.with_suffix(".so.tmp")
+        _run([HIPCC, *HIP_FLAGS, "-shared", *map(str, objs), "-o", str(tmp)])
+        os.replace(tmp, CAPI_LIB)
+    finally:
+        for obj in objs:
+            obj.unlink(missing_ok=True)
     return CAPI_LIB
 
 

@@ -1,4 +1,5 @@
-"""ctypes view of the C ABI in include/pmkl_attn.h (libpmkl_attn.so).
+"""ctypes view of the C ABI in include/pmkl_attn.h and include/pmkl_softmax.h
+(libpmkl_attn.so).
 
 This is the thin Python handle on the drop-in boundary: it passes device
 pointers, sizes and a HIP stream, nothing else.  Loading fails loudly when the
@@ -20,7 +21,9 @@ PMKL_EINVAL = 1
 PMKL_EUNSUPPORTED = 2
 PMKL_EHIP = 3
 
-# Every symbol include/pmkl_attn.h declares.
+PMKL_SOFTMAX_MAX_ELEMENTS = 1024
+
+# Every symbol include/pmkl_attn.h and include/pmkl_softmax.h declare.
 EXPORTED_SYMBOLS = (
     "pmkl_attn_fwd",
     "pmkl_causal_attention_forward",
@@ -30,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "pmkl_attn_bwd_supported",
     "pmkl_last_error",
     "pmkl_abi_version",
+    "pmkl_softmax_fwd",
+    "pmkl_warp_softmax_forward",
 )
 
 
@@ -85,6 +90,21 @@ class AttnBwdArgs(ctypes.Structure):
     ]
 
 
+class SoftmaxArgs(ctypes.Structure):
+    """Mirror of pmkl_softmax_args."""
+
+    _fields_ = [
+        ("dst", ctypes.c_void_p),
+        ("src", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int32),
+        ("in_dtype", ctypes.c_int32),
+        ("elements", ctypes.c_int64),
+        ("stride", ctypes.c_int64),
+        ("batch", ctypes.c_int64),
+        ("is_log", ctypes.c_int32),
+    ]
+
+
 class PmklError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"pmkl error {code}: {msg}")
@@ -122,6 +142,13 @@ def load() -> ctypes.CDLL:
     lib.pmkl_attn_bwd.restype = ctypes.c_int
     lib.pmkl_attn_bwd_supported.argtypes = [ctypes.c_int32, ctypes.c_int64]
     lib.pmkl_attn_bwd_supported.restype = ctypes.c_int
+    lib.pmkl_softmax_fwd.argtypes = [ctypes.POINTER(SoftmaxArgs), ctypes.c_void_p]
+    lib.pmkl_softmax_fwd.restype = ctypes.c_int
+    lib.pmkl_warp_softmax_forward.argtypes = [
+        ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+    ]
+    lib.pmkl_warp_softmax_forward.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -175,4 +202,20 @@ def make_bwd_args(dout, q, k, v, o, m, l, dq, dk, dv, workspace, workspace_bytes
     a.batch, a.heads, a.seq_len, a.head_dim = batch, heads, seq_len, head_dim
     a.scale = scale
     a.is_causal = 1 if is_causal else 0
+    return a
+
+
+def softmax_raw(args: SoftmaxArgs, stream: int | None = None) -> int:
+    """Call pmkl_softmax_fwd; returns the status code."""
+    return load().pmkl_softmax_fwd(ctypes.byref(args), ctypes.c_void_p(stream or 0))
+
+
+def make_softmax_args(dst, src, *, out_dtype: int, in_dtype: int, elements: int, stride: int, batch: int,
+                      is_log: bool = False) -> SoftmaxArgs:
+    """Build a SoftmaxArgs from raw integer pointers."""
+    a = SoftmaxArgs()
+    a.dst, a.src = dst, src
+    a.out_dtype, a.in_dtype = out_dtype, in_dtype
+    a.elements, a.stride, a.batch = elements, stride, batch
+    a.is_log = 1 if is_log else 0
     return a

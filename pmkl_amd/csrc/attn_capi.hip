@@ -19,36 +19,15 @@
 #include <cstring>
 
 #include "pmkl_attn.h"
+#include "capi_common.hpp"
 #include "attn_fwd_kernels.hpp"
 #include "attn_fwd_w64.hpp"
 #include "attn_bwd_kernels.hpp"
 
 namespace {
 
-thread_local char g_err[512] = "";
-
-int fail(int code, const char *file, int line, const char *fmt, ...) {
-    char msg[400];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(msg, sizeof(msg), fmt, ap);
-    va_end(ap);
-    const char *base = strrchr(file, '/');
-    snprintf(g_err, sizeof(g_err), "[pmkl check failed at %s:%d] %s", base ? base + 1 : file, line, msg);
-    return code;
-}
-
-#define PMKL_FAIL(code, ...) return fail((code), __FILE__, __LINE__, __VA_ARGS__)
-#define PMKL_REQUIRE(cond, code, ...) \
-    do {                              \
-        if (!(cond)) PMKL_FAIL((code), __VA_ARGS__); \
-    } while (0)
-
-size_t dtype_size(int32_t dt) { return dt == PMKL_DTYPE_F32 ? 4 : 2; }
-
-bool dtype_valid(int32_t dt) {
-    return dt == PMKL_DTYPE_F32 || dt == PMKL_DTYPE_F16 || dt == PMKL_DTYPE_BF16;
-}
+using pmkl_capi::dtype_size;
+using pmkl_capi::dtype_valid;
 
 bool head_dim_supported(int64_t d) { return d == 32 || d == 64 || d == 128; }
 
@@ -207,7 +186,7 @@ BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
 
 extern "C" {
 
-const char *pmkl_last_error(void) { return g_err; }
+const char *pmkl_last_error(void) { return pmkl_capi::g_err; }
 
 int pmkl_abi_version(void) { return PMKL_ABI_VERSION; }
 
@@ -216,7 +195,7 @@ int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim) {
 }
 
 int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
-    g_err[0] = '\0';
+    pmkl_capi::g_err[0] = '\0';
     PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
     PMKL_REQUIRE(dtype_valid(a->dtype), PMKL_EUNSUPPORTED, "unsupported dtype %d", (int)a->dtype);
     PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
@@ -313,7 +292,7 @@ int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim) {
 }
 
 int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
-    g_err[0] = '\0';
+    pmkl_capi::g_err[0] = '\0';
     PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
     PMKL_REQUIRE(a->dtype == PMKL_DTYPE_F16 || a->dtype == PMKL_DTYPE_BF16, PMKL_EUNSUPPORTED,
                  "backward dtype %d has no device kernel (supported: F16, BF16)", (int)a->dtype);

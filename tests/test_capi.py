@@ -1,4 +1,5 @@
-"""CPU tests of the C ABI (include/pmkl_attn.h, pmkl_amd/libpmkl_attn.so).
+"""CPU tests of the C ABI (include/pmkl_attn.h, include/pmkl_softmax.h,
+pmkl_amd/libpmkl_attn.so).
 
 No kernel is launched here: the library is loaded, every declared symbol is
 resolved, and the argument checks are driven into each of their error paths
@@ -17,12 +18,14 @@ import pytest
 from pmkl_amd import capi
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "pmkl_attn.h"
+HEADERS = (ROOT / "include" / "pmkl_attn.h", ROOT / "include" / "pmkl_softmax.h")
 
 
 def _declared_functions():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pmkl_\w+)\s*\(", text, re.M)))
+    names = set()
+    for header in HEADERS:
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pmkl_\w+)\s*\(", header.read_text(), re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_exported_set():
@@ -32,7 +35,7 @@ def test_header_declares_the_exported_set():
 def test_library_loads_and_exports_every_declared_symbol():
     lib = capi.load()
     for name in _declared_functions():
-        assert hasattr(lib, name), f"{name} is declared in pmkl_attn.h but not exported"
+        assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
 
 
 def test_abi_version_and_support_matrix():
@@ -164,3 +167,67 @@ def test_bwd_error_paths():
     _expect_bwd(_bwd_args(workspace_bytes=100), capi.PMKL_EINVAL, "workspace of 100 bytes is too small")
     # an empty problem succeeds without touching anything
     assert capi.attn_bwd_raw(_bwd_args(seq_len=0, dq=0, workspace=0)) == capi.PMKL_OK
+
+
+def test_softmax_args_struct_layout_matches_header(tmp_path):
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    fields = [f[0] for f in capi.SoftmaxArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("%s %zu\\n", "{f}", offsetof(pmkl_softmax_args, {f}));\n' for f in fields)
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "pmkl_softmax.h"\nint main(void) {\n'
+                   + body + '  printf("sizeof %zu\\n", sizeof(pmkl_softmax_args));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                         check=True).stdout.splitlines())
+    for f in fields:
+        assert int(out[f]) == getattr(capi.SoftmaxArgs, f).offset, f
+    assert int(out["sizeof"]) == ctypes.sizeof(capi.SoftmaxArgs)
+
+
+def _softmax_args(**kw):
+    base = dict(dst=0x1000, src=0x2000, out_dtype=capi.PMKL_DTYPE_F32, in_dtype=capi.PMKL_DTYPE_F32,
+                elements=1024, stride=1024, batch=12, is_log=False)
+    base.update(kw)
+    return capi.make_softmax_args(**base)
+
+
+def _expect_softmax(args, code, pattern):
+    rc = capi.softmax_raw(args)
+    msg = capi.last_error()
+    assert rc == code, (rc, msg)
+    assert re.search(pattern, msg), msg
+    assert re.search(r"pmkl check failed at softmax_capi\.hip:\d+", msg), msg
+
+
+def test_softmax_error_paths():
+    """The reference's CHECK_FAIL(softmax_elements >= 0 && <= 1024)
+    (warp_softmax.h:162) and this boundary's own argument checks."""
+    E = capi.PMKL_EINVAL
+    _expect_softmax(_softmax_args(elements=1025, stride=1025), E, r"softmax_elements <= 1024 \(got 1025\)")
+    _expect_softmax(_softmax_args(elements=-1), E, r"softmax_elements >= 0")
+    _expect_softmax(_softmax_args(in_dtype=7), E, r"unknown dtype")
+    _expect_softmax(_softmax_args(out_dtype=-1), E, r"unknown dtype")
+    _expect_softmax(_softmax_args(batch=-1), E, r"batch_count")
+    _expect_softmax(_softmax_args(batch=1 << 31), E, r"batch_count")
+    _expect_softmax(_softmax_args(stride=1000), E, r"stride \(1000\) < softmax_elements \(1024\)")
+    _expect_softmax(_softmax_args(src=0), E, r"null src or dst")
+    _expect_softmax(_softmax_args(dst=0x2000, out_dtype=capi.PMKL_DTYPE_BF16), E, r"in-place")
+    rc = capi.load().pmkl_softmax_fwd(None, None)
+    assert rc == E and "null argument block" in capi.last_error()
+
+
+def test_softmax_empty_problem_returns_ok_without_touching_pointers():
+    """softmax_elements == 0 returns early as in the reference
+    (warp_softmax.h:163-164); so does batch_count == 0."""
+    assert capi.softmax_raw(_softmax_args(dst=0, src=0, elements=0, stride=0)) == capi.PMKL_OK
+    assert capi.softmax_raw(_softmax_args(dst=0, src=0, batch=0)) == capi.PMKL_OK
+    lib = capi.load()
+    assert lib.pmkl_warp_softmax_forward(0, 0, 0, None, None, 0, 0, 5, None) == capi.PMKL_OK
+    assert lib.pmkl_warp_softmax_forward(0, 0, 0, None, None, 1025, 1025, 5, None) == capi.PMKL_EINVAL
+    assert "softmax_elements" in capi.last_error()
