@@ -258,8 +258,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
             for (int dk = 0; dk < NDK; ++dk)
                 qf[qb][dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(src + 16 * dk));
         }
-        // Defined in AGPRs, where the QK MFMAs read them: otherwise the
-        // register allocator may keep them in VGPRs and copy before each use.
+    };
+    // Q defined in AGPRs, where the QK MFMAs read them (otherwise the register
+    // allocator may keep them in VGPRs and copy before each use).  The pin
+    // waits for the loads, so it sits after the previous item's O stores:
+    // the load latency overlaps them.
+    auto pin_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -524,7 +528,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
 
-    // Epilogue of an item: normalise, store O, m, l.
+    // Epilogue of an item: normalise, store O, m, l.  In the O^T accumulator
+    // lane (col, hi) holds dims 32 db + 8 g4 + 4 hi + 0..3 of query row col;
+    // one v_permlane32_swap per packed pair hands lane col the partner's
+    // dims +4..7 of g4 = 2j and lane col + 32 lane col's dims +8..11 of
+    // g4 = 2j + 1, so each lane stores 8 consecutive dims (16 bytes) and a
+    // row's 32-byte piece is written by two lanes of one store instruction.
     auto store_item = [&](int bh_e, int q0w_e, bool active_e) __attribute__((always_inline)) {
         const int b_ = bh_e / p.H, h_ = bh_e - b_ * p.H;
         T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
@@ -532,19 +541,25 @@ void attn_fwd_w64_kernel(AttnParams p) {
         for (int qb = 0; qb < 2; ++qb) {
             const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
             const int qi = q0w_e + 32 * qb + col;
-            if (active_e && qi < S) {
-                const float inv = 1.0f / l_sum;
+            const bool ok = active_e && qi < S;
+            const float inv = 1.0f / l_sum;                    // not stored where !ok
+            T *orow = og + (int64_t)(ok ? qi : 0) * p.o_ss;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const f32x16_t &c = acc[qb][db];
+                    const uint32_t a0 = E::pack2(c[8 * j] * inv, c[8 * j + 1] * inv);
+                    const uint32_t a1 = E::pack2(c[8 * j + 2] * inv, c[8 * j + 3] * inv);
+                    const uint32_t b0 = E::pack2(c[8 * j + 4] * inv, c[8 * j + 5] * inv);
+                    const uint32_t b1 = E::pack2(c[8 * j + 6] * inv, c[8 * j + 7] * inv);
+                    const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+                    const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+                    const u32x4_t w4 = {r0[0], r1[0], r0[1], r1[1]};
+                    if (ok) *(u32x4_t *)(orow + 32 * db + 16 * j + 8 * hi) = w4;
+                }
+            if (ok) {
                 const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
-                T *orow = og + (int64_t)qi * p.o_ss;
-#pragma unroll
-                for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4) {
-                        const int d = 32 * db + 8 * g4 + 4 * hi;
-                        u32x2_t w2 = {E::pack2(acc[qb][db][4 * g4] * inv, acc[qb][db][4 * g4 + 1] * inv),
-                                      E::pack2(acc[qb][db][4 * g4 + 2] * inv, acc[qb][db][4 * g4 + 3] * inv)};
-                        *(u32x2_t *)(orow + d) = w2;
-                    }
                 if (hi == 0) {
                     const int64_t mi = (int64_t)bh_e * S + qi;
                     const float mval = m_true[qb] * p.scale;
@@ -584,6 +599,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     int sa = 0, sb = 1, sc3 = 2;
 
     while (true) {
+        pin_q();
         // Scores and maxima of tile 0 (slot sa; landed, see above).
         reset_state();
         {
