@@ -81,8 +81,15 @@ template <> struct W64Mma<_Float16> {
     }
 };
 // 24 wait states: enough between an MFMA writing registers and VALU reading
-// or writing them, for every MFMA used here.
+// or writing them, for every MFMA used here.  The MFMAs are inline asm, so
+// the compiler inserts no wait states of its own and does not know that the
+// drain guards their results: every drain is followed (and, where VALU
+// writes feed a later MFMA, preceded) by w64_fence on the registers it
+// guards, an empty asm that redefines them, so no read of them is scheduled
+// above the drain and no write below it.
 __device__ __forceinline__ void w64_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+__device__ __forceinline__ void w64_fence_a(f32x16_t &x) { asm volatile("" : "+a"(x)); }
+__device__ __forceinline__ void w64_fence_v(f32x16_t &x) { asm volatile("" : "+v"(x)); }
 
 // s = (R <= d) ? s : -inf, through VCC: left to itself the compiler computes
 // all compares of a tile into separate SGPR pairs first, and that pressure
@@ -446,6 +453,11 @@ void attn_fwd_w64_kernel(AttnParams p) {
             moff[qb] = up ? mo : moff[qb];
         }
     };
+    // The O^T accumulators of block qb at a drain.
+    auto fence_block = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) w64_fence_a(acc[qb][db]);
+    };
     auto apply_rescale = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -453,10 +465,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 l_a[qb] *= alpha[qb];
                 l_b[qb] *= alpha[qb];
                 w64_mfma_drain();
+                fence_block(qb);
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) acc[qb][db][r] *= alpha[qb];
+                fence_block(qb);
                 w64_mfma_drain();
                 rescale[qb] = false;
             }
@@ -582,6 +596,10 @@ void attn_fwd_w64_kernel(AttnParams p) {
             });
             if constexpr (s == Sch::MS0) {
                 w64_mfma_drain();   // the QK MFMAs of tile t+1 have written the scores
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) w64_fence_v(sc[SET ^ 1][qb][kb]);
                 sm_mask(t + 1, NSET{});
             }
             if constexpr (s < Sch::ES)
@@ -646,6 +664,10 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 }
             }
             w64_mfma_drain();
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) w64_fence_v(sc[0][qb][kb]);
             sm_mask(0, S0{});
 #pragma unroll
             for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
@@ -680,6 +702,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
             sc3 = tmp;
         }
         w64_mfma_drain();   // the last PV MFMAs have written O
+        fence_block(0);
+        fence_block(1);
 
         // Next item first (its Q loads overlap this item's epilogue), then
         // this item's outputs: m, l now, O staged for the next item's first
