@@ -173,6 +173,39 @@ def test_many_items_per_workgroup(device, B, H, S, D, dtype, causal):
     _say(f"{tag}: {errs}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("slope", [2.0, 0.4])
+@pytest.mark.parametrize("causal", [True, False])
+def test_running_max_grows_every_tile(device, dtype, slope, causal):
+    """Scores that rise along the keys (s_ij ~ slope * j plus noise): the
+    running row max grows on every key tile (slope 2: by ~128 per 64 keys,
+    past the 16-bit kernels' lazy-rescale threshold each tile; slope 0.4:
+    every other tile), so the O^T accumulators are rescaled over and over
+    between MFMAs.  Several work items per workgroup (B H = 260 heads)."""
+    import torch
+
+    from pmkl_amd.workloads import torch_dtype
+    from tests.parity import check_outputs
+
+    B, H, S, D = 2, 130, 512, 128
+    tag = f"{dtype} slope {slope} causal={causal}"
+    _say(f"case {tag}")
+    g = torch.Generator().manual_seed(91)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    a = (slope * D ** 0.5) ** 0.5          # |q| * |k_j| / sqrt(D) = slope * j
+    j = torch.arange(S, dtype=torch.float32)
+    q = a * u.expand(B, H, S, D) + 0.3 * torch.randn(B, H, S, D, generator=g)
+    k = (a * j[:, None]) * u
+    k = k.expand(B, H, S, D) + 0.3 * torch.randn(B, H, S, D, generator=g)
+    v = torch.randn(B, H, S, D, generator=g)
+    q, k, v = (x.to(torch_dtype(dtype)) for x in (q, k, v))
+    o, m, l = _run_capi(q, k, v, device, causal=causal)
+    rows = _sample_rows(S, 24, seed=int(slope * 10) + causal)
+    errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)
+    _say(f"{tag}: {errs}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
 def test_closed_forms(device, dtype):
     """K == 0: O_i = mean(V_0..V_i), m_i = 0, l_i = i + 1 (every tile, diagonal included).
