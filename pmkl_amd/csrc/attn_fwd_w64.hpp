@@ -151,8 +151,6 @@ template <int D> struct W64Sched {
 
     // DMAs of the iteration, all before the barrier.
     static constexpr int dma_slot(int j, int n) { return 1 + j * (BARS - 1) / n; }
-    // Stores of the previous item's O (first two iterations), after the barrier.
-    static constexpr int store_slot(int k, int n) { return BARS + 1 + k * (NSLOT - 1 - BARS) / n; }
 
     static constexpr bool valid() {
         for (int n = 0; n < NU; ++n)
@@ -341,11 +339,6 @@ void attn_fwd_w64_kernel(AttnParams p) {
     float alpha[2];
     bool rescale[2];
     float l_a[2], l_b[2];      // two partial row sums per block
-    // O of the previous item, normalised and packed, waiting to be stored in
-    // the first two iterations of the next item (see stage_item).
-    u32x4_t ost[2][NDB][2];    // [qb][db][j]: dims 32 db + 16 j + 8 hi .. + 7
-    T *orow_st[2] = {nullptr, nullptr};
-    bool ok_st[2] = {false, false};
     const float lazy_raw = kLazyLog2 / p.scale_log2;
     auto reset_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -494,69 +487,6 @@ void attn_fwd_w64_kernel(AttnParams p) {
         }
     };
 
-    // Epilogue of an item: normalise O into ost, store m, l.  In the O^T
-    // accumulator lane (col, hi) holds dims 32 db + 8 g4 + 4 hi + 0..3 of
-    // query row col; one v_permlane32_swap per packed pair hands lane col the
-    // partner's dims +4..7 of g4 = 2j and lane col + 32 lane col's dims
-    // +8..11 of g4 = 2j + 1, so each lane stores 8 consecutive dims (16 bytes)
-    // and a row's 32-byte piece is written by two lanes of one instruction.
-    // The O stores themselves are issued later (flush_half): every workgroup
-    // reaches its item boundaries at about the same time, and written in one
-    // burst O saturates HBM writes while the waves wait.
-    auto stage_item = [&](int bh_e, int q0w_e, bool active_e) __attribute__((always_inline)) {
-        const int b_ = bh_e / p.H, h_ = bh_e - b_ * p.H;
-        T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
-            const int qi = q0w_e + 32 * qb + col;
-            const bool ok = active_e && qi < S;
-            const float inv = 1.0f / l_sum;                    // not stored where !ok
-            ok_st[qb] = ok;
-            orow_st[qb] = og + (int64_t)(ok ? qi : 0) * p.o_ss;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const f32x16_t &c = acc[qb][db];
-                    const uint32_t a0 = E::pack2(c[8 * j] * inv, c[8 * j + 1] * inv);
-                    const uint32_t a1 = E::pack2(c[8 * j + 2] * inv, c[8 * j + 3] * inv);
-                    const uint32_t b0 = E::pack2(c[8 * j + 4] * inv, c[8 * j + 5] * inv);
-                    const uint32_t b1 = E::pack2(c[8 * j + 6] * inv, c[8 * j + 7] * inv);
-                    const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-                    const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-                    ost[qb][db][j] = u32x4_t{r0[0], r1[0], r0[1], r1[1]};
-                }
-            if (ok) {
-                const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
-                if (hi == 0) {
-                    const int64_t mi = (int64_t)bh_e * S + qi;
-                    const float mval = m_true[qb] * p.scale;
-                    if (p.ml_f32) {
-                        ((float *)p.m)[mi] = mval;
-                        ((float *)p.l)[mi] = l_tot;
-                    } else {
-                        ((T *)p.m)[mi] = (T)mval;
-                        ((T *)p.l)[mi] = (T)l_tot;
-                    }
-                }
-            }
-        }
-    };
-    // Store chunk k (0 .. 2 NDB - 1) of block qb of the staged O.
-    auto flush_chunk = [&](int qb, int k) __attribute__((always_inline)) {
-        const int db = k >> 1, j = k & 1;
-        if (ok_st[qb]) *(u32x4_t *)(orow_st[qb] + 32 * db + 16 * j + 8 * hi) = ost[qb][db][j];
-    };
-    auto flush_all = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-            for (int k = 0; k < 2 * NDB; ++k) flush_chunk(qb, k);
-            ok_st[qb] = false;
-        }
-    };
-
     frag ring[RING];
     // Iteration t (tile scores in set SET = t & 1): QK of tile t+1 into set
     // SET ^ 1 and PV of tile t, with the VALU work of the schedule.  LDS
@@ -609,20 +539,59 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 constexpr int k = decltype(k_c)::value;
                 if constexpr (Sch::max_slot(k) == s) max_unit(NSET{}, k);
             });
-            // The previous item's O: block SET in iteration SET of this item,
-            // after the barrier, so each store has an iteration to complete
-            // before the next DMA wait counts it.
-            w64_static_for<0, 2 * NDB>([&](auto k_c) __attribute__((always_inline)) {
-                constexpr int k = decltype(k_c)::value;
-                if constexpr (Sch::store_slot(k, 2 * NDB) == s)
-                    if (t < 2) flush_chunk(SET, k);
-            });
             __builtin_amdgcn_sched_barrier(0);
         });
         apply_rescale();   // decided for tile t+1; the PV MFMAs of tile t are issued
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
+
+    // Epilogue of an item: normalise, store O, m, l.  In the O^T accumulator
+    // lane (col, hi) holds dims 32 db + 8 g4 + 4 hi + 0..3 of query row col;
+    // one v_permlane32_swap per packed pair hands lane col the partner's
+    // dims +4..7 of g4 = 2j and lane col + 32 lane col's dims +8..11 of
+    // g4 = 2j + 1, so each lane stores 8 consecutive dims (16 bytes) and a
+    // row's 32-byte piece is written by two lanes of one store instruction.
+    auto store_item = [&](int bh_e, int q0w_e, bool active_e) __attribute__((always_inline)) {
+        const int b_ = bh_e / p.H, h_ = bh_e - b_ * p.H;
+        T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
+            const int qi = q0w_e + 32 * qb + col;
+            const bool ok = active_e && qi < S;
+            const float inv = 1.0f / l_sum;                    // not stored where !ok
+            T *orow = og + (int64_t)(ok ? qi : 0) * p.o_ss;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const f32x16_t &c = acc[qb][db];
+                    const uint32_t a0 = E::pack2(c[8 * j] * inv, c[8 * j + 1] * inv);
+                    const uint32_t a1 = E::pack2(c[8 * j + 2] * inv, c[8 * j + 3] * inv);
+                    const uint32_t b0 = E::pack2(c[8 * j + 4] * inv, c[8 * j + 5] * inv);
+                    const uint32_t b1 = E::pack2(c[8 * j + 6] * inv, c[8 * j + 7] * inv);
+                    const auto r0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+                    const auto r1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+                    const u32x4_t w4 = {r0[0], r1[0], r0[1], r1[1]};
+                    if (ok) *(u32x4_t *)(orow + 32 * db + 16 * j + 8 * hi) = w4;
+                }
+            if (ok) {
+                const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
+                if (hi == 0) {
+                    const int64_t mi = (int64_t)bh_e * S + qi;
+                    const float mval = m_true[qb] * p.scale;
+                    if (p.ml_f32) {
+                        ((float *)p.m)[mi] = mval;
+                        ((float *)p.l)[mi] = l_tot;
+                    } else {
+                        ((T *)p.m)[mi] = (T)mval;
+                        ((T *)p.l)[mi] = (T)l_tot;
+                    }
+                }
+            }
+        }
+    };
 
     // ---- first item: K(0), V(0), K(1) landed; K(2), V(1) in flight ----
     int r = 0;
@@ -682,7 +651,6 @@ void attn_fwd_w64_kernel(AttnParams p) {
 
         // ---- tiles the wave computes, two per iteration (score sets 0, 1) ----
         int t = 0;
-        if (ntw2 == 0) flush_all();   // no iteration to carry the previous item's O
         for (; t < ntw2; t += 2) {
             iteration(t, S0{}, sa, sb, sc3);
             iteration(t + 1, S1{}, sb, sc3, sa);
@@ -706,8 +674,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
         fence_block(1);
 
         // Next item first (its Q loads overlap this item's epilogue), then
-        // this item's outputs: m, l now, O staged for the next item's first
-        // iterations (all of it now after the last item).
+        // this item's outputs.
         const int bh_e = bh, q0w_e = q0w;
         const bool active_e = wave_active, more = has_next;
         if (more) {
@@ -716,11 +683,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
             set_next(item_index(r + 1));
             load_q();
         }
-        stage_item(bh_e, q0w_e, active_e);
-        if (!more) {
-            flush_all();
-            break;
-        }
+        store_item(bh_e, q0w_e, active_e);
+        if (!more) break;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no DMA outlives the workgroup
 }
