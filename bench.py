@@ -243,7 +243,7 @@ def bench_softmax(args):
     avg_ms = ev0.elapsed_time(ev1) / args.steps
     alg_bytes = rows * n * (4 + 4)
     achieved = alg_bytes / (avg_ms / 1e3) / 1e9
-    kernel = "softmax_fwd_kernel<float, float, 4, 4, false>"
+    kernel = "softmax_fwd_kernel<float,float,4,4,false>"
     cpu = None
     if not args.no_cpu:
         from oracle import oracle
