@@ -43,22 +43,23 @@ struct BwdParams {
     float *lse2;                        // workspace [BH, S]: m * log2(e) + log2(l)
     float *drow;                        // workspace [BH, S]: D_n
     int32_t S, BH;
-    int32_t n_qtiles, n_ktiles;         // ceil(S / owned rows per workgroup)
+    int32_t n_qtiles, n_ktiles;         // ceil(S / owned rows per workgroup), dq and dk/dv kernels
     float scale, scale_log2;
     int32_t ml_f32;                     // m, l stored as float (else in T)
 };
 
 // Waves per workgroup: 8 (two per SIMD) where the registers of a wave fit in
-// 256; at head_dim 128 the owned rows' fragments and the dK/dV accumulators
-// need more, so 4 waves (one per SIMD, up to 512 registers).
-template <int D> constexpr int bwd_waves() { return D >= 128 ? 4 : 8; }
+// 256, else 4 (one per SIMD, up to 512 registers): at head_dim 128 the
+// pipelined dQ loop (two score sets) and the dK/dV accumulators.
+template <int D> constexpr int bwd_waves_dq() { return D >= 128 ? 4 : 8; }
+template <int D> constexpr int bwd_waves_dkdv() { return D >= 128 ? 4 : 8; }
 
 // 16-byte chunk (logical chunk pc of row `row`) staging of a 64-row tile:
 // loads go to registers two tiles ahead, LDS writes place the chunk at its
 // swizzled position in each layout the tensor is read with.
-template <typename T, int D>
+template <typename T, int D, int NW_>
 struct BwdTile {
-    static constexpr int NW = bwd_waves<D>();
+    static constexpr int NW = NW_;
     static constexpr int THREADS = NW * 64;
     static constexpr int ROWS = 32 * NW;        // owned rows per workgroup
     static constexpr int BN = 64;
@@ -118,16 +119,19 @@ __device__ __forceinline__ float bwd_load_ml(const void *base, int64_t i, bool f
 // pass 1: dQ (and the row vectors D_n, log2-sum-exp)
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(BwdParams p) {
     using E = Elt16<T>;
     using frag = typename E::frag;
-    using TL = BwdTile<T, D>;
+    using TL = BwdTile<T, D, bwd_waves_dq<D>()>;
     constexpr int BN = TL::BN, CPR = TL::CPR, LOADS = TL::LOADS;
     constexpr int kBwdThreads = TL::THREADS, kBwdRows = TL::ROWS;
     constexpr bool PARTIAL = TL::PARTIAL;
     constexpr int NDB = D / 32, NDK = D / 16;
 
-    __shared__ __attribute__((aligned(16))) T smem[2][3][BN * D];   // [stage][K swz_k, K swz_v, V swz_k]
+    // The software-pipelined loop (head_dim 128, one wave per SIMD) keeps three
+    // tiles in LDS, the plain loop two.
+    constexpr bool PIPE = D >= 128;
+    __shared__ __attribute__((aligned(16))) T smem[PIPE ? 3 : 2][3][BN * D];   // [stage][K swz_k, K swz_v, V swz_k]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -168,35 +172,61 @@ __global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(Bwd
     const float lse2 = m_i * 1.4426950408889634f + __log2f(l_i);
     const float c = p.scale_log2;
 
-    // ---- staging ----
-    u32x4_t kreg[2][LOADS], vreg[2][LOADS];
+    // ---- staging: tile kt lives in LDS stage kt % 3; the registers hold the
+    // tile two ahead of the one being computed ----
+    u32x4_t kreg[LOADS], vreg[LOADS];
     int goff[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         const int sl = j * kBwdThreads + tid;
         goff[j] = ((sl / CPR) * D + 8 * (sl % CPR)) * (int)sizeof(T);
     }
-    auto gload = [&](int kt, auto set_c) __attribute__((always_inline)) {
+    auto gload = [&](int kt) __attribute__((always_inline)) {
+        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S);
+        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S);
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j)
+            if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
+                kreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[j], 0, 0));
+                vreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[j], 0, 0));
+            }
+    };
+    auto swrite = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int sl = j * kBwdThreads + tid;
+            if (!PARTIAL || sl < TL::CHUNKS) {
+                const int row = sl / CPR, pc = sl % CPR;
+                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = kreg[j];
+                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = kreg[j];
+                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = vreg[j];
+            }
+        }
+    };
+
+    // ---- staging of the plain loop: two register sets, two LDS stages ----
+    u32x4_t kreg2[2][LOADS], vreg2[2][LOADS];
+    auto gload2 = [&](int kt, auto set_c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
         const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S);
         const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S);
 #pragma unroll
         for (int j = 0; j < LOADS; ++j)
             if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
-                kreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[j], 0, 0));
-                vreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[j], 0, 0));
+                kreg2[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[j], 0, 0));
+                vreg2[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[j], 0, 0));
             }
     };
-    auto swrite = [&](int st, auto set_c) __attribute__((always_inline)) {
+    auto swrite2 = [&](int st, auto set_c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) {
             const int sl = j * kBwdThreads + tid;
             if (!PARTIAL || sl < TL::CHUNKS) {
                 const int row = sl / CPR, pc = sl % CPR;
-                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = kreg[SET][j];
-                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = kreg[SET][j];
-                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = vreg[SET][j];
+                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = kreg2[SET][j];
+                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = kreg2[SET][j];
+                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = vreg2[SET][j];
             }
         }
     };
@@ -214,17 +244,122 @@ __global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(Bwd
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
 
-    // One loop over the key tiles.  PASS 0: D_n; PASS 1: dS and dQ.
+    // Scores S^T and dP^T of a tile: MFMA m (0 .. NSD-1) is (dk, kb, which)
+    // = (m / 4, (m / 2) % 2, m % 2), i.e. four interleaved accumulator chains.
+    constexpr int NSD = 4 * NDK;
+    auto sd_frag = [&](int st, int m) __attribute__((always_inline)) {
+        const int dk = m >> 2, kb = (m >> 1) & 1, which = m & 1;
+        return bwd_row_frag<T, D>(smem[st][which ? 2 : 0], kb, dk, arow, hi);
+    };
+    auto sd_mma = [&](f32x16_t (&sv)[2], f32x16_t (&dpv)[2], int m, frag a) __attribute__((always_inline)) {
+        const int dk = m >> 2, kb = (m >> 1) & 1, which = m & 1;
+        if (which) dpv[kb] = E::mma(a, df[dk], dk == 0 ? f32x16_t{} : dpv[kb]);
+        else sv[kb] = E::mma(a, qf[dk], dk == 0 ? f32x16_t{} : sv[kb]);
+    };
+    // All scores of tile (stage st), fragments read one MFMA ahead.
+    auto sd_tile = [&](f32x16_t (&sv)[2], f32x16_t (&dpv)[2], int st) __attribute__((always_inline)) {
+        frag a = sd_frag(st, 0);
+#pragma unroll
+        for (int m = 0; m < NSD; ++m) {
+            const frag b = m + 1 < NSD ? sd_frag(st, m + 1) : a;
+            sd_mma(sv, dpv, m, a);
+            a = b;
+        }
+    };
+
+    // One loop over the key tiles.  PASS 0: D_n; PASS 1: dS and dQ.  Software
+    // pipelined by one tile: step kt issues the S^T, dP^T MFMAs of tile kt+1
+    // one by one, each followed by a share of tile kt's softmax VALU (P, dS),
+    // with the MFMA fragments read RING MFMAs ahead; then the dQ MFMAs of
+    // tile kt, then tile kt+2 goes from registers to LDS and tile kt+3 is
+    // loaded.  One barrier per tile.
+    constexpr int RING = 4;
+    constexpr int NUNIT = 16;   // softmax units of a tile: (kb, register pair)
     auto key_loop = [&](auto pass_c) __attribute__((always_inline)) {
         constexpr int PASS = decltype(pass_c)::value;
-        gload(0, std::integral_constant<int, 0>{});
-        swrite(0, std::integral_constant<int, 0>{});
+        gload(0);
+        swrite(0);
+        gload(min(1, nt - 1));
+        swrite(1);
+        gload(min(2, nt - 1));
+        __syncthreads();
+        f32x16_t s0[2], dp0[2], s1[2], dp1[2];
+        if (wave_active) sd_tile(s0, dp0, 0);
+
+        auto step = [&](int kt, f32x16_t (&sc)[2], f32x16_t (&dpc)[2], f32x16_t (&sn)[2], f32x16_t (&dpn)[2])
+                        __attribute__((always_inline)) {
+            const int st = kt % 3, st1 = (kt + 1) % 3;
+            const int kbase = kt * BN;
+            const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
+            if (wave_needed) {
+                const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+                const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
+                uint32_t dsk[2][8];
+                frag ring[RING];
+#pragma unroll
+                for (int i = 0; i < RING; ++i) ring[i] = sd_frag(st1, i);
+#pragma unroll
+                for (int m = 0; m < NSD; ++m) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    sd_mma(sn, dpn, m, ring[m % RING]);
+                    if (m + RING < NSD) ring[m % RING] = sd_frag(st1, m + RING);
+                    // softmax units of tile kt behind this MFMA
+#pragma unroll
+                    for (int u = (m * NUNIT) / NSD; u < ((m + 1) * NUNIT) / NSD; ++u) {
+                        const int kb = u >> 3, r = 2 * (u & 7);
+                        float pv[2];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int key = kbase + 32 * kb + 16 * hi + r + e;
+                            const float sv = need_mask && key > lim ? -INFINITY : sc[kb][r + e];
+                            pv[e] = fast_exp2(__builtin_fmaf(sv, c, -lse2));
+                        }
+                        if (PASS == 0) {
+                            drow_part = __builtin_fmaf(pv[0], dpc[kb][r], drow_part);
+                            drow_part = __builtin_fmaf(pv[1], dpc[kb][r + 1], drow_part);
+                        } else {
+                            dsk[kb][r >> 1] = E::pack2(pv[0] * (dpc[kb][r] - drow), pv[1] * (dpc[kb][r + 1] - drow));
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (PASS == 1) {
+                    // dQ^T += K^T dS^T over the 4 blocks of 16 keys
+                    const T *Kv = smem[st][1];
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int cc = 0; cc < 2; ++cc) {
+                            u32x4_t bw = {dsk[kb][4 * cc], dsk[kb][4 * cc + 1], dsk[kb][4 * cc + 2], dsk[kb][4 * cc + 3]};
+                            const frag bfr = __builtin_bit_cast(frag, bw);
+#pragma unroll
+                            for (int db = 0; db < NDB; ++db)
+                                acc[db] = E::mma(bwd_tr_frag<T, D>(Kv, kb, cc, db, vrow0, vcol0), bfr, acc[db]);
+                        }
+                }
+            }
+            if (kt + 2 < nt) swrite((kt + 2) % 3);
+            if (kt + 3 < nt) gload(kt + 3);
+            __syncthreads();
+        };
+        for (int kt = 0; kt < nt; kt += 2) {
+            step(kt, s0, dp0, s1, dp1);
+            if (kt + 1 < nt) step(kt + 1, s1, dp1, s0, dp0);
+        }
+    };
+
+    // The plain loop (head_dim < 128, two waves per SIMD): per tile S^T and
+    // dP^T, then P / dS, then dQ, the other wave of the SIMD overlapping.
+    auto key_loop_plain = [&](auto pass_c) __attribute__((always_inline)) {
+        constexpr int PASS = decltype(pass_c)::value;
+        gload2(0, std::integral_constant<int, 0>{});
+        swrite2(0, std::integral_constant<int, 0>{});
         __builtin_amdgcn_s_waitcnt(0);
-        gload(min(1, nt - 1), std::integral_constant<int, 1>{});
+        gload2(min(1, nt - 1), std::integral_constant<int, 1>{});
         __syncthreads();
         auto tile_step = [&](auto set_c, int kt) __attribute__((always_inline)) {
             constexpr int SET = decltype(set_c)::value;
-            gload(min(kt + 2, nt - 1), set_c);
+            gload2(min(kt + 2, nt - 1), set_c);
             const int kbase = kt * BN;
             const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
             if (wave_needed) {
@@ -278,7 +413,7 @@ __global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(Bwd
                         }
                 }
             }
-            if (kt + 1 < nt) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
+            if (kt + 1 < nt) swrite2(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
             __syncthreads();
         };
         for (int kt = 0; kt < nt; kt += 2) {
@@ -299,14 +434,16 @@ __global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(Bwd
         }
         drow = half_sum(part);
     } else {
-        key_loop(std::integral_constant<int, 0>{});
+        if constexpr (PIPE) key_loop(std::integral_constant<int, 0>{});
+        else key_loop_plain(std::integral_constant<int, 0>{});
         drow = half_sum(drow_part);
     }
     if (hi == 0 && qi < S) {
         p.lse2[(int64_t)bh * S + qi] = lse2;
         p.drow[(int64_t)bh * S + qi] = drow;
     }
-    key_loop(std::integral_constant<int, 1>{});
+    if constexpr (PIPE) key_loop(std::integral_constant<int, 1>{});
+    else key_loop_plain(std::integral_constant<int, 1>{});
 
     // ---- epilogue: dq = scale * dQ^T, lane = query column ----
     if (wave_active && qi < S) {
@@ -327,10 +464,10 @@ __global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dq_kernel(Bwd
 // pass 2: dK, dV
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(bwd_waves<D>() * 64, 1) void attn_bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_kernel(BwdParams p) {
     using E = Elt16<T>;
     using frag = typename E::frag;
-    using TL = BwdTile<T, D>;
+    using TL = BwdTile<T, D, bwd_waves_dkdv<D>()>;
     constexpr int BN = TL::BN, CPR = TL::CPR, LOADS = TL::LOADS;
     constexpr int kBwdThreads = TL::THREADS, kBwdRows = TL::ROWS;
     constexpr bool PARTIAL = TL::PARTIAL;

@@ -156,17 +156,19 @@ typedef void (*bwd_kernel_fn)(BwdParams);
 
 struct BwdKernels {
     bwd_kernel_fn dq, dkdv;
-    int threads, rows;   // threads and owned rows per workgroup
+    int dq_threads, dq_rows;       // threads and owned rows per workgroup
+    int dkdv_threads, dkdv_rows;
 };
 
 template <typename T, int D>
 BwdKernels pick_bwd(bool causal) {
-    using TL = pmkl_amd::BwdTile<T, D>;
+    using TQ = pmkl_amd::BwdTile<T, D, pmkl_amd::bwd_waves_dq<D>()>;
+    using TK = pmkl_amd::BwdTile<T, D, pmkl_amd::bwd_waves_dkdv<D>()>;
     if (causal)
-        return {pmkl_amd::attn_bwd_dq_kernel<T, D, true>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, true>, TL::THREADS,
-                TL::ROWS};
-    return {pmkl_amd::attn_bwd_dq_kernel<T, D, false>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, false>, TL::THREADS,
-            TL::ROWS};
+        return {pmkl_amd::attn_bwd_dq_kernel<T, D, true>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, true>, TQ::THREADS,
+                TQ::ROWS, TK::THREADS, TK::ROWS};
+    return {pmkl_amd::attn_bwd_dq_kernel<T, D, false>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, false>, TQ::THREADS,
+            TQ::ROWS, TK::THREADS, TK::ROWS};
 }
 
 BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
@@ -179,7 +181,7 @@ BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
         if (d == 64) return pick_bwd<_Float16, 64>(causal);
         if (d == 128) return pick_bwd<_Float16, 128>(causal);
     }
-    return {nullptr, nullptr, 0, 0};
+    return {nullptr, nullptr, 0, 0, 0, 0};
 }
 
 }  // namespace
@@ -333,9 +335,9 @@ int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
     const BwdKernels kc = select_bwd(a->dtype, D, a->is_causal != 0);
     PMKL_REQUIRE(kc.dq != nullptr, PMKL_EUNSUPPORTED, "no backward kernel for dtype %d head_dim %lld",
                  (int)a->dtype, (long long)D);
-    const int64_t ntiles = (S + kc.rows - 1) / kc.rows;
-    PMKL_REQUIRE(ntiles * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
-                 (long long)(ntiles * B * H));
+    const int64_t nq = (S + kc.dq_rows - 1) / kc.dq_rows, nk = (S + kc.dkdv_rows - 1) / kc.dkdv_rows;
+    PMKL_REQUIRE(std::max(nq, nk) * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
+                 (long long)(std::max(nq, nk) * B * H));
 
     BwdParams p;
     p.q = a->q;
@@ -352,18 +354,18 @@ int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
     p.drow = (float *)a->workspace + B * H * S;
     p.S = (int32_t)S;
     p.BH = (int32_t)(B * H);
-    p.n_qtiles = (int32_t)ntiles;
-    p.n_ktiles = (int32_t)ntiles;
+    p.n_qtiles = (int32_t)nq;
+    p.n_ktiles = (int32_t)nk;
     p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
     p.scale_log2 = p.scale * 1.4426950408889634f;
     p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
 
     hipStream_t st = (hipStream_t)stream;
     // dQ first: it writes the row vectors the dK/dV pass reads.
-    hipLaunchKernelGGL(kc.dq, dim3((unsigned)(ntiles * B * H)), dim3(kc.threads), 0, st, p);
+    hipLaunchKernelGGL(kc.dq, dim3((unsigned)(nq * B * H)), dim3(kc.dq_threads), 0, st, p);
     hipError_t err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dq kernel launch failed: %s", hipGetErrorString(err));
-    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)(ntiles * B * H)), dim3(kc.threads), 0, st, p);
+    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)(nk * B * H)), dim3(kc.dkdv_threads), 0, st, p);
     err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dk/dv kernel launch failed: %s", hipGetErrorString(err));
     return PMKL_OK;
