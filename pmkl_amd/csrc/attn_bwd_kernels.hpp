@@ -324,18 +324,24 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if (PASS == 1) {
-                    // dQ^T += K^T dS^T over the 4 blocks of 16 keys
+                    // dQ^T += K^T dS^T over the 4 blocks of 16 keys: MFMA m is
+                    // (kb, cc, db) = (m / (2 NDB), (m / NDB) % 2, m % NDB), its
+                    // transposed K fragment read RING MFMAs ahead
                     const T *Kv = smem[st][1];
+                    constexpr int NQ = 4 * NDB;
+                    auto kt_frag = [&](int m) __attribute__((always_inline)) {
+                        return bwd_tr_frag<T, D>(Kv, m / (2 * NDB), (m / NDB) & 1, m % NDB, vrow0, vcol0);
+                    };
+                    frag qring[RING];
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
+                    for (int i = 0; i < RING; ++i) qring[i] = kt_frag(i);
 #pragma unroll
-                        for (int cc = 0; cc < 2; ++cc) {
-                            u32x4_t bw = {dsk[kb][4 * cc], dsk[kb][4 * cc + 1], dsk[kb][4 * cc + 2], dsk[kb][4 * cc + 3]};
-                            const frag bfr = __builtin_bit_cast(frag, bw);
-#pragma unroll
-                            for (int db = 0; db < NDB; ++db)
-                                acc[db] = E::mma(bwd_tr_frag<T, D>(Kv, kb, cc, db, vrow0, vcol0), bfr, acc[db]);
-                        }
+                    for (int m = 0; m < NQ; ++m) {
+                        const int kb = m / (2 * NDB), cc = (m / NDB) & 1, db = m % NDB;
+                        const u32x4_t bw = {dsk[kb][4 * cc], dsk[kb][4 * cc + 1], dsk[kb][4 * cc + 2], dsk[kb][4 * cc + 3]};
+                        acc[db] = E::mma(qring[m % RING], __builtin_bit_cast(frag, bw), acc[db]);
+                        if (m + RING < NQ) qring[m % RING] = kt_frag(m + RING);
+                    }
                 }
             }
             if (kt + 2 < nt) swrite((kt + 2) % 3);
