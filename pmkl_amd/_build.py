@@ -28,9 +28,6 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # Builtin MFMAs in VGPR form: the 64-row kernel's scores are read by VALU
-    # softmax; its O accumulators are pinned to AGPRs by inline asm instead.
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 CAPI_LIB = PKG / "libpmkl_attn.so"

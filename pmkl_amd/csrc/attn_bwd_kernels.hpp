@@ -595,15 +595,24 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
             const T *Ov = smem[SET][3];
             const float *lse2s = svec[SET][0];
             const float *drows = svec[SET][1];
+            // S = Q K^T, dP = dout V^T: MFMA m is (dk, qb, which) = (m / 4,
+            // (m / 2) % 2, m % 2), four interleaved chains, row fragments read
+            // RING MFMAs ahead
+            constexpr int RING = 2, NSD = 4 * NDK;
+            auto sd_frag = [&](int m) __attribute__((always_inline)) {
+                return bwd_row_frag<T, D>((m & 1) ? Ok : Qk, (m >> 1) & 1, m >> 2, arow, hi);
+            };
             f32x16_t s[2], dp[2];
+            {
+                frag ring[RING];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
+                for (int i = 0; i < RING; ++i) ring[i] = sd_frag(i);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) s[qb][r] = dp[qb][r] = 0.f;
-#pragma unroll
-                for (int dk = 0; dk < NDK; ++dk) {
-                    s[qb] = E::mma(bwd_row_frag<T, D>(Qk, qb, dk, arow, hi), kf[dk], s[qb]);
-                    dp[qb] = E::mma(bwd_row_frag<T, D>(Ok, qb, dk, arow, hi), vf[dk], dp[qb]);
+                for (int m = 0; m < NSD; ++m) {
+                    const int dk = m >> 2, qb = (m >> 1) & 1;
+                    if (m & 1) dp[qb] = E::mma(ring[m % RING], vf[dk], dk == 0 ? f32x16_t{} : dp[qb]);
+                    else s[qb] = E::mma(ring[m % RING], kf[dk], dk == 0 ? f32x16_t{} : s[qb]);
+                    if (m + RING < NSD) ring[m % RING] = sd_frag(m + RING);
                 }
             }
             // register r of block qb holds query qbase + 32 qb + 16 hi + r
@@ -633,21 +642,31 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
                     dsp[qb][r >> 1] = E::pack2(dsv[0], dsv[1]);
                 }
             }
-            // dV^T += dout^T P,  dK^T += Q^T dS over the 4 blocks of 16 queries
+            // dV^T += dout^T P,  dK^T += Q^T dS over the 4 blocks of 16 queries:
+            // MFMA m is (qb, cc, db, which), transposed fragments read RING
+            // MFMAs ahead
+            constexpr int NGR = 8 * NDB;
+            auto gr_frag = [&](int m) __attribute__((always_inline)) {
+                const int db = (m >> 1) % NDB, cc = (m / (2 * NDB)) & 1, qb = m / (4 * NDB);
+                return bwd_tr_frag<T, D>((m & 1) ? Qv : Ov, qb, cc, db, vrow0, vcol0);
+            };
+            {
+                frag ring[RING];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
+                for (int i = 0; i < RING; ++i) ring[i] = gr_frag(i);
 #pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                    u32x4_t bp = {pp[qb][4 * cc], pp[qb][4 * cc + 1], pp[qb][4 * cc + 2], pp[qb][4 * cc + 3]};
-                    u32x4_t bs = {dsp[qb][4 * cc], dsp[qb][4 * cc + 1], dsp[qb][4 * cc + 2], dsp[qb][4 * cc + 3]};
-                    const frag fp = __builtin_bit_cast(frag, bp);
-                    const frag fs = __builtin_bit_cast(frag, bs);
-#pragma unroll
-                    for (int db = 0; db < NDB; ++db) {
-                        dv_acc[db] = E::mma(bwd_tr_frag<T, D>(Ov, qb, cc, db, vrow0, vcol0), fp, dv_acc[db]);
-                        dk_acc[db] = E::mma(bwd_tr_frag<T, D>(Qv, qb, cc, db, vrow0, vcol0), fs, dk_acc[db]);
+                for (int m = 0; m < NGR; ++m) {
+                    const int db = (m >> 1) % NDB, cc = (m / (2 * NDB)) & 1, qb = m / (4 * NDB);
+                    if (m & 1) {
+                        const u32x4_t bs = {dsp[qb][4 * cc], dsp[qb][4 * cc + 1], dsp[qb][4 * cc + 2], dsp[qb][4 * cc + 3]};
+                        dk_acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bs), dk_acc[db]);
+                    } else {
+                        const u32x4_t bp = {pp[qb][4 * cc], pp[qb][4 * cc + 1], pp[qb][4 * cc + 2], pp[qb][4 * cc + 3]};
+                        dv_acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bp), dv_acc[db]);
                     }
+                    if (m + RING < NGR) ring[m % RING] = gr_frag(m + RING);
                 }
+            }
         }
         if (it + 1 < ntl) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
         __syncthreads();
