@@ -98,7 +98,12 @@ int pmkl_softmax_fwd(const pmkl_softmax_args *a, void *stream) {
     PMKL_REQUIRE(a->src != nullptr && a->dst != nullptr, PMKL_EINVAL, "null src or dst");
     PMKL_REQUIRE(a->src != a->dst || a->in_dtype == a->out_dtype, PMKL_EINVAL,
                  "in-place softmax needs the same input and output dtype");
-    PMKL_REQUIRE(a->stride <= (int64_t(1) << 40), PMKL_EINVAL, "stride too large (%lld)", (long long)a->stride);
+    // Element offsets r * stride + i stay far inside int64 (and inside any
+    // allocation): the span (batch - 1) * stride + elements is capped at 2^48.
+    PMKL_REQUIRE(a->stride <= (int64_t(1) << 48) &&
+                     (a->batch - 1) <= ((int64_t(1) << 48) - a->elements) / (a->stride > 0 ? a->stride : 1),
+                 PMKL_EINVAL, "rows span more than 2^48 elements (batch %lld, stride %lld)", (long long)a->batch,
+                 (long long)a->stride);
 
     const int64_t n = a->elements;
     const int wv = 16 / (int)pmkl_capi::dtype_size(a->in_dtype);

@@ -217,6 +217,8 @@ def test_softmax_error_paths():
     _expect_softmax(_softmax_args(batch=1 << 31), E, r"batch_count")
     _expect_softmax(_softmax_args(stride=1000), E, r"stride \(1000\) < softmax_elements \(1024\)")
     _expect_softmax(_softmax_args(src=0), E, r"null src or dst")
+    _expect_softmax(_softmax_args(stride=1 << 40, batch=1 << 20), E, r"rows span more than 2\^48")
+    _expect_softmax(_softmax_args(stride=(1 << 48) + 1, batch=1), E, r"rows span more than 2\^48")
     _expect_softmax(_softmax_args(dst=0x2000, out_dtype=capi.PMKL_DTYPE_BF16), E, r"in-place")
     rc = capi.load().pmkl_softmax_fwd(None, None)
     assert rc == E and "null argument block" in capi.last_error()
