@@ -469,6 +469,15 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
 // ---------------------------------------------------------------------------
 // pass 2: dK, dV
 // ---------------------------------------------------------------------------
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled at compile time.
+template <int B, int E, typename F>
+__device__ __forceinline__ void bwd_static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        bwd_static_for<B + 1, E>(f);
+    }
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_kernel(BwdParams p) {
     using E = Elt16<T>;
@@ -522,44 +531,42 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
     const float c = p.scale_log2;
 
     // ---- staging of Q, dout (two layouts each) and the row vectors ----
-    u32x4_t qreg[2][LOADS], oreg[2][LOADS];
-    float vreg[2];   // one row-vector element per thread (threads 0..127)
+    u32x4_t qreg[LOADS], oreg[LOADS];
+    float vreg;      // one row-vector element per thread (threads 0..127)
     int goff[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         const int sl = j * kBwdThreads + tid;
         goff[j] = ((sl / CPR) * D + 8 * (sl % CPR)) * (int)sizeof(T);
     }
-    auto gload = [&](int qtl, auto set_c) __attribute__((always_inline)) {
-        constexpr int SET = decltype(set_c)::value;
+    auto gload = [&](int qtl) __attribute__((always_inline)) {
         const auto qr = bwd_rows_rsrc<T, D>(qg, qtl * BN, S);
         const auto orr = bwd_rows_rsrc<T, D>(dog, qtl * BN, S);
 #pragma unroll
         for (int j = 0; j < LOADS; ++j)
             if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
-                qreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qr, goff[j], 0, 0));
-                oreg[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(orr, goff[j], 0, 0));
+                qreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qr, goff[j], 0, 0));
+                oreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(orr, goff[j], 0, 0));
             }
         if (tid < 2 * BN) {
             const int row = qtl * BN + (tid & (BN - 1));
             // rows past S: lse2 = +inf gives P = 0 (their scores are masked too)
-            vreg[SET] = row < S ? ((tid < BN) ? lse2g[row] : drowg[row]) : ((tid < BN) ? INFINITY : 0.f);
+            vreg = row < S ? ((tid < BN) ? lse2g[row] : drowg[row]) : ((tid < BN) ? INFINITY : 0.f);
         }
     };
-    auto swrite = [&](int st, auto set_c) __attribute__((always_inline)) {
-        constexpr int SET = decltype(set_c)::value;
+    auto swrite = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < LOADS; ++j) {
             const int sl = j * kBwdThreads + tid;
             if (!PARTIAL || sl < TL::CHUNKS) {
                 const int row = sl / CPR, pc = sl % CPR;
-                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = qreg[SET][j];
-                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = qreg[SET][j];
-                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = oreg[SET][j];
-                *(u32x4_t *)(&smem[st][3][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = oreg[SET][j];
+                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = qreg[j];
+                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = qreg[j];
+                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = oreg[j];
+                *(u32x4_t *)(&smem[st][3][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = oreg[j];
             }
         }
-        if (tid < 2 * BN) svec[st][tid >> 6][tid & (BN - 1)] = vreg[SET];
+        if (tid < 2 * BN) svec[st][tid >> 6][tid & (BN - 1)] = vreg;
     };
 
     const int arow = key_of_arow(col);
@@ -575,16 +582,20 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
 
     const int ntl = nq - t0;   // query tiles of the workgroup
     if (ntl > 0) {
-        gload(t0, std::integral_constant<int, 0>{});
-        swrite(0, std::integral_constant<int, 0>{});
+        gload(t0);
+        swrite(0);
         __builtin_amdgcn_s_waitcnt(0);
-        gload(min(t0 + 1, nq - 1), std::integral_constant<int, 1>{});
+        gload(min(t0 + 1, nq - 1));
         __syncthreads();
     }
     auto tile_step = [&](auto set_c, int it) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
         const int qtl = t0 + it;
-        gload(min(qtl + 2, nq - 1), set_c);
+        // Tile it+1 goes from registers to the LDS stage that tile it-1 used
+        // (free since the barrier that ended tile it-1), then tile it+2 is
+        // loaded into the same registers: one register set, a tile of latency.
+        if (it + 1 < ntl) swrite(SET ^ 1);
+        gload(min(qtl + 2, nq - 1));
         const int qbase = qtl * BN;
         // causal: the tile holds a query at or past the wave's first key
         const bool wave_needed = wave_active && (!CAUSAL || qbase + BN - 1 >= k0w);
@@ -595,80 +606,169 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
             const T *Ov = smem[SET][3];
             const float *lse2s = svec[SET][0];
             const float *drows = svec[SET][1];
-            // S = Q K^T, dP = dout V^T: MFMA m is (dk, qb, which) = (m / 4,
-            // (m / 2) % 2, m % 2), four interleaved chains, row fragments read
-            // RING MFMAs ahead
-            constexpr int RING = 2, NSD = 4 * NDK;
-            auto sd_frag = [&](int m) __attribute__((always_inline)) {
-                return bwd_row_frag<T, D>((m & 1) ? Ok : Qk, (m >> 1) & 1, m >> 2, arow, hi);
-            };
-            f32x16_t s[2], dp[2];
-            {
-                frag ring[RING];
-#pragma unroll
-                for (int i = 0; i < RING; ++i) ring[i] = sd_frag(i);
-#pragma unroll
-                for (int m = 0; m < NSD; ++m) {
-                    const int dk = m >> 2, qb = (m >> 1) & 1;
-                    if (m & 1) dp[qb] = E::mma(ring[m % RING], vf[dk], dk == 0 ? f32x16_t{} : dp[qb]);
-                    else s[qb] = E::mma(ring[m % RING], kf[dk], dk == 0 ? f32x16_t{} : s[qb]);
-                    if (m + RING < NSD) ring[m % RING] = sd_frag(m + RING);
-                }
-            }
-            // register r of block qb holds query qbase + 32 qb + 16 hi + r
-            const bool need_mask = (CAUSAL && qbase < k0w + 31) || (qbase + BN > S);
-            uint32_t pp[2][8], dsp[2][8];
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                const int rb = 32 * qb + 16 * hi;
-                f32x4_t l4[4], d4[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    l4[i] = *(const f32x4_t *)(lse2s + rb + 4 * i);
-                    d4[i] = *(const f32x4_t *)(drows + rb + 4 * i);
-                }
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
+            if constexpr (D >= 128) {
+                // Half-tile pipeline over the two 32-query blocks qb: one stream of
+                // NMM MFMAs in four phases,
+                //   0  S, dP of block 0
+                //   1  S, dP of block 1        + P, dS of block 0 behind the MFMAs
+                //   2  dV^T, dK^T of block 0   + P, dS of block 1 behind the MFMAs
+                //   3  dV^T, dK^T of block 1
+                // so the softmax VALU of one block runs under the other block's
+                // MFMAs.  S, dP MFMA j of a block is (dk, which) = (j / 2, j % 2);
+                // dV^T, dK^T MFMA j is (cc, db, which) = (j / (2 NDB),
+                // (j / 2) % NDB, j % 2).  Fragments are read RING MFMAs ahead.
+                constexpr int RING = 2, NSQ = 2 * NDK, NGQ = 4 * NDB, NMM = 2 * (NSQ + NGQ);
+                auto frag_at = [&](int n) __attribute__((always_inline)) {
+                    if (n < 2 * NSQ) {
+                        const int qb = n / NSQ, j = n % NSQ;
+                        return bwd_row_frag<T, D>((j & 1) ? Ok : Qk, qb, j >> 1, arow, hi);
+                    }
+                    const int m = n - 2 * NSQ, qb = m / NGQ, j = m % NGQ;
+                    return bwd_tr_frag<T, D>((j & 1) ? Qv : Ov, qb, j / (2 * NDB), (j >> 1) % NDB, vrow0, vcol0);
+                };
+                // register r of block qb holds query qbase + 32 qb + 16 hi + r
+                const bool need_mask = (CAUSAL && qbase < k0w + 31) || (qbase + BN > S);
+                f32x16_t s[2], dp[2];
+                uint32_t pp[2][8], dsp[2][8];
+                f32x4_t l4[2][4], d4[2][4];
+                auto load_vec = [&](int qb) __attribute__((always_inline)) {
+                    const int rb = 32 * qb + 16 * hi;
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        l4[qb][i] = *(const f32x4_t *)(lse2s + rb + 4 * i);
+                        d4[qb][i] = *(const f32x4_t *)(drows + rb + 4 * i);
+                    }
+                };
+                // P and dS of registers 2u, 2u + 1 of block qb
+                auto unit = [&](int qb, int u) __attribute__((always_inline)) {
+                    const int rb = 32 * qb + 16 * hi, r = 2 * u;
                     float pv[2], dsv[2];
-#pragma unroll
+    #pragma unroll
                     for (int e = 0; e < 2; ++e) {
                         const int q = qbase + rb + r + e;
                         const bool vis = !need_mask || (q < S && (!CAUSAL || q >= kj));
                         const float sv = vis ? s[qb][r + e] : -INFINITY;
-                        pv[e] = fast_exp2(__builtin_fmaf(sv, c, -l4[(r + e) >> 2][(r + e) & 3]));
-                        dsv[e] = pv[e] * (dp[qb][r + e] - d4[(r + e) >> 2][(r + e) & 3]);
+                        pv[e] = fast_exp2(__builtin_fmaf(sv, c, -l4[qb][(r + e) >> 2][(r + e) & 3]));
+                        dsv[e] = pv[e] * (dp[qb][r + e] - d4[qb][(r + e) >> 2][(r + e) & 3]);
                     }
-                    pp[qb][r >> 1] = E::pack2(pv[0], pv[1]);
-                    dsp[qb][r >> 1] = E::pack2(dsv[0], dsv[1]);
-                }
-            }
-            // dV^T += dout^T P,  dK^T += Q^T dS over the 4 blocks of 16 queries:
-            // MFMA m is (qb, cc, db, which), transposed fragments read RING
-            // MFMAs ahead
-            constexpr int NGR = 8 * NDB;
-            auto gr_frag = [&](int m) __attribute__((always_inline)) {
-                const int db = (m >> 1) % NDB, cc = (m / (2 * NDB)) & 1, qb = m / (4 * NDB);
-                return bwd_tr_frag<T, D>((m & 1) ? Qv : Ov, qb, cc, db, vrow0, vcol0);
-            };
-            {
-                frag ring[RING];
-#pragma unroll
-                for (int i = 0; i < RING; ++i) ring[i] = gr_frag(i);
-#pragma unroll
-                for (int m = 0; m < NGR; ++m) {
-                    const int db = (m >> 1) % NDB, cc = (m / (2 * NDB)) & 1, qb = m / (4 * NDB);
-                    if (m & 1) {
-                        const u32x4_t bs = {dsp[qb][4 * cc], dsp[qb][4 * cc + 1], dsp[qb][4 * cc + 2], dsp[qb][4 * cc + 3]};
-                        dk_acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bs), dk_acc[db]);
+                    pp[qb][u] = E::pack2(pv[0], pv[1]);
+                    dsp[qb][u] = E::pack2(dsv[0], dsv[1]);
+                };
+                auto mma_at = [&](int n, frag a) __attribute__((always_inline)) {
+                    if (n < 2 * NSQ) {
+                        const int qb = n / NSQ, j = n % NSQ, dk = j >> 1;
+                        if (j & 1) dp[qb] = E::mma(a, vf[dk], dk == 0 ? f32x16_t{} : dp[qb]);
+                        else s[qb] = E::mma(a, kf[dk], dk == 0 ? f32x16_t{} : s[qb]);
                     } else {
-                        const u32x4_t bp = {pp[qb][4 * cc], pp[qb][4 * cc + 1], pp[qb][4 * cc + 2], pp[qb][4 * cc + 3]};
-                        dv_acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bp), dv_acc[db]);
+                        const int m = n - 2 * NSQ, qb = m / NGQ, j = m % NGQ;
+                        const int db = (j >> 1) % NDB, cc = j / (2 * NDB);
+                        if (j & 1) {
+                            const u32x4_t bs = {dsp[qb][4 * cc], dsp[qb][4 * cc + 1], dsp[qb][4 * cc + 2], dsp[qb][4 * cc + 3]};
+                            dk_acc[db] = E::mma(a, __builtin_bit_cast(frag, bs), dk_acc[db]);
+                        } else {
+                            const u32x4_t bp = {pp[qb][4 * cc], pp[qb][4 * cc + 1], pp[qb][4 * cc + 2], pp[qb][4 * cc + 3]};
+                            dv_acc[db] = E::mma(a, __builtin_bit_cast(frag, bp), dv_acc[db]);
+                        }
                     }
-                    if (m + RING < NGR) ring[m % RING] = gr_frag(m + RING);
+                };
+                frag ring[RING];
+    #pragma unroll
+                for (int i = 0; i < RING; ++i) ring[i] = frag_at(i);
+                // a block's row vectors are read from LDS a few MFMAs before its
+                // first softmax unit
+                constexpr int VLEAD = NSQ < 4 ? NSQ : 4;
+                bwd_static_for<0, NMM>([&](auto n_c) __attribute__((always_inline)) {
+                    constexpr int n = decltype(n_c)::value;
+                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (n == NSQ - VLEAD) load_vec(0);
+                    if constexpr (n == 2 * NSQ - VLEAD) load_vec(1);
+                    mma_at(n, ring[n % RING]);
+                    if constexpr (n + RING < NMM) ring[n % RING] = frag_at(n + RING);
+                    // phase 1 carries block 0's units, phase 2 block 1's
+                    constexpr int ph = n < NSQ ? 0 : n < 2 * NSQ ? 1 : n < 2 * NSQ + NGQ ? 2 : 3;
+                    if constexpr (ph == 1 || ph == 2) {
+                        constexpr int len = ph == 1 ? NSQ : NGQ, k = n - (ph == 1 ? NSQ : 2 * NSQ);
+    #pragma unroll
+                        for (int u = (k * 8) / len; u < ((k + 1) * 8) / len; ++u) unit(ph - 1, u);
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                // Plain tile (the half-tile pipeline spills at 8 waves):
+                // S = Q K^T, dP = dout V^T: MFMA m is (dk, qb, which) = (m / 4,
+                // (m / 2) % 2, m % 2), four interleaved chains, row fragments read
+                // RING MFMAs ahead
+                constexpr int RING = 2, NSD = 4 * NDK;
+                auto sd_frag = [&](int m) __attribute__((always_inline)) {
+                    return bwd_row_frag<T, D>((m & 1) ? Ok : Qk, (m >> 1) & 1, m >> 2, arow, hi);
+                };
+                f32x16_t s[2], dp[2];
+                {
+                    frag ring[RING];
+    #pragma unroll
+                    for (int i = 0; i < RING; ++i) ring[i] = sd_frag(i);
+    #pragma unroll
+                    for (int m = 0; m < NSD; ++m) {
+                        const int dk = m >> 2, qb = (m >> 1) & 1;
+                        if (m & 1) dp[qb] = E::mma(ring[m % RING], vf[dk], dk == 0 ? f32x16_t{} : dp[qb]);
+                        else s[qb] = E::mma(ring[m % RING], kf[dk], dk == 0 ? f32x16_t{} : s[qb]);
+                        if (m + RING < NSD) ring[m % RING] = sd_frag(m + RING);
+                    }
+                }
+                // register r of block qb holds query qbase + 32 qb + 16 hi + r
+                const bool need_mask = (CAUSAL && qbase < k0w + 31) || (qbase + BN > S);
+                uint32_t pp[2][8], dsp[2][8];
+    #pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    const int rb = 32 * qb + 16 * hi;
+                    f32x4_t l4[4], d4[4];
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        l4[i] = *(const f32x4_t *)(lse2s + rb + 4 * i);
+                        d4[i] = *(const f32x4_t *)(drows + rb + 4 * i);
+                    }
+    #pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        float pv[2], dsv[2];
+    #pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int q = qbase + rb + r + e;
+                            const bool vis = !need_mask || (q < S && (!CAUSAL || q >= kj));
+                            const float sv = vis ? s[qb][r + e] : -INFINITY;
+                            pv[e] = fast_exp2(__builtin_fmaf(sv, c, -l4[(r + e) >> 2][(r + e) & 3]));
+                            dsv[e] = pv[e] * (dp[qb][r + e] - d4[(r + e) >> 2][(r + e) & 3]);
+                        }
+                        pp[qb][r >> 1] = E::pack2(pv[0], pv[1]);
+                        dsp[qb][r >> 1] = E::pack2(dsv[0], dsv[1]);
+                    }
+                }
+                // dV^T += dout^T P,  dK^T += Q^T dS over the 4 blocks of 16 queries:
+                // MFMA m is (qb, cc, db, which), transposed fragments read RING
+                // MFMAs ahead
+                constexpr int NGR = 8 * NDB;
+                auto gr_frag = [&](int m) __attribute__((always_inline)) {
+                    const int db = (m >> 1) % NDB, cc = (m / (2 * NDB)) & 1, qb = m / (4 * NDB);
+                    return bwd_tr_frag<T, D>((m & 1) ? Qv : Ov, qb, cc, db, vrow0, vcol0);
+                };
+                {
+                    frag ring[RING];
+    #pragma unroll
+                    for (int i = 0; i < RING; ++i) ring[i] = gr_frag(i);
+    #pragma unroll
+                    for (int m = 0; m < NGR; ++m) {
+                        const int db = (m >> 1) % NDB, cc = (m / (2 * NDB)) & 1, qb = m / (4 * NDB);
+                        if (m & 1) {
+                            const u32x4_t bs = {dsp[qb][4 * cc], dsp[qb][4 * cc + 1], dsp[qb][4 * cc + 2], dsp[qb][4 * cc + 3]};
+                            dk_acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bs), dk_acc[db]);
+                        } else {
+                            const u32x4_t bp = {pp[qb][4 * cc], pp[qb][4 * cc + 1], pp[qb][4 * cc + 2], pp[qb][4 * cc + 3]};
+                            dv_acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bp), dv_acc[db]);
+                        }
+                        if (m + RING < NGR) ring[m % RING] = gr_frag(m + RING);
+                    }
                 }
             }
         }
-        if (it + 1 < ntl) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
         __syncthreads();
     };
     for (int it = 0; it < ntl; it += 2) {
