@@ -10,7 +10,7 @@ if str(ROOT) not in sys.path:
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (runs under gpurun / at round end)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU")
 
 
 @pytest.fixture(scope="session")
