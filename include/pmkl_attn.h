@@ -125,7 +125,8 @@ typedef struct pmkl_attn_bwd_args {
                             pmkl_attn_bwd_workspace_size() bytes; scratch of
                             the call (two floats per query row)               */
     uint64_t workspace_bytes;
-    int32_t dtype;       /* pmkl_dtype of dout, q, k, v, o, dq, dk, dv: F16 or BF16 */
+    int32_t dtype;       /* pmkl_dtype of dout, q, k, v, o, dq, dk, dv: F32, F16
+                            or BF16 (F32: m and l in F32 too)                 */
     int32_t ml_dtype;    /* pmkl_dtype of m and l: dtype or F32                 */
     int64_t batch;
     int64_t heads;

@@ -23,6 +23,7 @@
 #include "attn_fwd_kernels.hpp"
 #include "attn_fwd_w64.hpp"
 #include "attn_bwd_kernels.hpp"
+#include "attn_bwd_f32.hpp"
 
 namespace {
 
@@ -158,6 +159,7 @@ struct BwdKernels {
     bwd_kernel_fn dq, dkdv;
     int dq_threads, dq_rows;       // threads and owned rows per workgroup
     int dkdv_threads, dkdv_rows;
+    bool flat;                     // grid over the B*H*S rows, else (row tile, head)
 };
 
 template <typename T, int D>
@@ -166,9 +168,19 @@ BwdKernels pick_bwd(bool causal) {
     using TK = pmkl_amd::BwdTile<T, D, pmkl_amd::bwd_waves_dkdv<D>()>;
     if (causal)
         return {pmkl_amd::attn_bwd_dq_kernel<T, D, true>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, true>, TQ::THREADS,
-                TQ::ROWS, TK::THREADS, TK::ROWS};
+                TQ::ROWS, TK::THREADS, TK::ROWS, false};
     return {pmkl_amd::attn_bwd_dq_kernel<T, D, false>, pmkl_amd::attn_bwd_dkdv_kernel<T, D, false>, TQ::THREADS,
-            TQ::ROWS, TK::THREADS, TK::ROWS};
+            TQ::ROWS, TK::THREADS, TK::ROWS, false};
+}
+
+template <int D>
+BwdKernels pick_bwd_f32(bool causal) {
+    constexpr int W = pmkl_amd::kBwdF32Waves;
+    if (causal)
+        return {pmkl_amd::attn_bwd_f32_dq_kernel<D, true>, pmkl_amd::attn_bwd_f32_dkdv_kernel<D, true>, 64 * W, W,
+                64 * W, W, true};
+    return {pmkl_amd::attn_bwd_f32_dq_kernel<D, false>, pmkl_amd::attn_bwd_f32_dkdv_kernel<D, false>, 64 * W, W,
+            64 * W, W, true};
 }
 
 BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
@@ -180,8 +192,12 @@ BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
         if (d == 32) return pick_bwd<_Float16, 32>(causal);
         if (d == 64) return pick_bwd<_Float16, 64>(causal);
         if (d == 128) return pick_bwd<_Float16, 128>(causal);
+    } else if (dt == PMKL_DTYPE_F32) {
+        if (d == 32) return pick_bwd_f32<32>(causal);
+        if (d == 64) return pick_bwd_f32<64>(causal);
+        if (d == 128) return pick_bwd_f32<128>(causal);
     }
-    return {nullptr, nullptr, 0, 0, 0, 0};
+    return {nullptr, nullptr, 0, 0, 0, 0, false};
 }
 
 }  // namespace
@@ -290,14 +306,14 @@ uint64_t pmkl_attn_bwd_workspace_size(int64_t batch, int64_t heads, int64_t seq_
 }
 
 int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim) {
-    return (dtype == PMKL_DTYPE_F16 || dtype == PMKL_DTYPE_BF16) && head_dim_supported(head_dim) ? 1 : 0;
+    return dtype_valid(dtype) && head_dim_supported(head_dim) ? 1 : 0;
 }
 
 int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
     pmkl_capi::g_err[0] = '\0';
     PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
-    PMKL_REQUIRE(a->dtype == PMKL_DTYPE_F16 || a->dtype == PMKL_DTYPE_BF16, PMKL_EUNSUPPORTED,
-                 "backward dtype %d has no device kernel (supported: F16, BF16)", (int)a->dtype);
+    PMKL_REQUIRE(dtype_valid(a->dtype), PMKL_EUNSUPPORTED,
+                 "backward dtype %d has no device kernel (supported: F32, F16, BF16)", (int)a->dtype);
     PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
                  "ml_dtype %d must equal dtype %d or be F32", (int)a->ml_dtype, (int)a->dtype);
     PMKL_REQUIRE(a->batch >= 0 && a->heads >= 0 && a->seq_len >= 0, PMKL_EINVAL,
@@ -336,8 +352,11 @@ int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
     PMKL_REQUIRE(kc.dq != nullptr, PMKL_EUNSUPPORTED, "no backward kernel for dtype %d head_dim %lld",
                  (int)a->dtype, (long long)D);
     const int64_t nq = (S + kc.dq_rows - 1) / kc.dq_rows, nk = (S + kc.dkdv_rows - 1) / kc.dkdv_rows;
-    PMKL_REQUIRE(std::max(nq, nk) * B * H <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
-                 (long long)(std::max(nq, nk) * B * H));
+    // workgroups of each kernel
+    const int64_t gq = kc.flat ? (B * H * S + kc.dq_rows - 1) / kc.dq_rows : nq * B * H;
+    const int64_t gk = kc.flat ? (B * H * S + kc.dkdv_rows - 1) / kc.dkdv_rows : nk * B * H;
+    PMKL_REQUIRE(std::max(gq, gk) <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
+                 (long long)std::max(gq, gk));
 
     BwdParams p;
     p.q = a->q;
@@ -362,10 +381,10 @@ int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
 
     hipStream_t st = (hipStream_t)stream;
     // dQ first: it writes the row vectors the dK/dV pass reads.
-    hipLaunchKernelGGL(kc.dq, dim3((unsigned)(nq * B * H)), dim3(kc.dq_threads), 0, st, p);
+    hipLaunchKernelGGL(kc.dq, dim3((unsigned)gq), dim3(kc.dq_threads), 0, st, p);
     hipError_t err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dq kernel launch failed: %s", hipGetErrorString(err));
-    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)(nk * B * H)), dim3(kc.dkdv_threads), 0, st, p);
+    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)gk), dim3(kc.dkdv_threads), 0, st, p);
     err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dk/dv kernel launch failed: %s", hipGetErrorString(err));
     return PMKL_OK;

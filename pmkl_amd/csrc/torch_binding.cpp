@@ -261,8 +261,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_bw(const at:
     TORCH_CHECK(q.is_cuda(), "fused_self_attention_bw: tensors must be on the CPU or a ROCm device, got ",
                 q.device());
     const int32_t dt = to_pmkl_dtype(q.scalar_type());
-    TORCH_CHECK(pmkl_attn_bwd_supported(dt, D), "fused_self_attention_bw: the device backward supports float16 ",
-                "and bfloat16 with head_dim 32, 64 or 128, got ", q.scalar_type(), " head_dim ", D);
+    TORCH_CHECK(pmkl_attn_bwd_supported(dt, D), "fused_self_attention_bw: the device backward supports float32, ",
+                "float16 and bfloat16 with head_dim 32, 64 or 128, got ", q.scalar_type(), " head_dim ", D);
     if (B * H * S == 0) return std::forward_as_tuple(dq, dk, dv);
     const int32_t mdt = to_pmkl_dtype(out_m.scalar_type());
     TORCH_CHECK(out_m.scalar_type() == out_l.scalar_type() && (mdt == dt || mdt == PMKL_DTYPE_F32),

@@ -48,8 +48,8 @@ class fused_self_attention_(Function):
     def backward(ctx, grad_output, grad_m, grad_l):
         q, k, v, out, out_m, out_l = ctx.saved_tensors
         if q.is_cuda:
-            if q.dtype not in (torch.float16, torch.bfloat16):
-                raise NotImplementedError(f"the device backward supports float16 and bfloat16, got {q.dtype}")
+            if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+                raise NotImplementedError(f"the device backward supports float32, float16 and bfloat16, got {q.dtype}")
             from .. import attn_bwd
 
             dq, dk, dv = attn_bwd(grad_output.contiguous(), q.contiguous(), k.contiguous(), v.contiguous(),

@@ -6,10 +6,15 @@ The device forward runs first and its m, l (in the tensor dtype, as the
 reference's autograd saves them) feed both the device backward and the
 oracle, so both use the same probabilities P = exp(s - m) / l.
 
-Tolerance: the kernels round P and dS to the tensor dtype for the MFMA
-products and round dq, dk, dv on output; accumulation is fp32.  Each
+Tolerance: the 16-bit kernels round P and dS to the tensor dtype for the
+MFMA products and round dq, dk, dv on output; accumulation is fp32.  Each
 gradient tensor is held to max|g - g_ref| <= TOL * max|g_ref| (+ the half-ulp
 output rounding of each element), TOL = 1.5e-2 for bf16 and 3e-3 for fp16.
+The fp32 kernels keep every product and sum in fp32: TOL = 1e-5, relative
+to the larger of max|g_ref| and the magnitude of the summed terms (for dq:
+scale * max over (i, d) of sum_j P_ij (|dP_ij| + |D_i|) |k_jd|; dk alike with
+q; dv: max of sum_i P_ij |dout_id|), because dP - D cancels: at S = 1 the
+exact dq is 0 and both sides return rounding noise of that magnitude.
 """
 from __future__ import annotations
 
@@ -22,8 +27,8 @@ from oracle import oracle
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"bf16": 1.5e-2, "fp16": 3e-3}
-MANT = {"bf16": 7, "fp16": 10}
+TOL = {"bf16": 1.5e-2, "fp16": 3e-3, "fp32": 1e-5}
+MANT = {"bf16": 7, "fp16": 10, "fp32": 23}
 
 
 def _say(msg):
@@ -54,14 +59,37 @@ def _run(B, H, S, D, dtype, causal, seed, with_o=False, dist="normal", heads=Non
     ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), _np(m).reshape(B * H, S), _np(l).reshape(B * H, S),
                           causal=causal, heads=heads)
     got = [r(x) if heads is None else r(x)[list(heads)] for x in (dq, dk, dv)]
-    return got, ref
+    if dtype == "fp32":
+        hs = list(range(B * H)) if heads is None else list(heads)
+        fl = _term_floors(r(q)[hs], r(k)[hs], r(v)[hs], r(do)[hs], _np(m).reshape(B * H, S)[hs],
+                          _np(l).reshape(B * H, S)[hs], causal)
+        return got, ref, fl
+    return got, ref, (0.0, 0.0, 0.0)
 
 
-def _check(got, ref, dtype, label):
+def _term_floors(q, k, v, do, m, l, causal):
+    """Magnitudes of the summed terms of dq, dk, dv (float64, [BH, S, D]
+    inputs, default scale): the error scale of an fp32 sum with cancellation."""
+    sc = 1.0 / np.sqrt(q.shape[-1])
+    fl = np.zeros(3)
+    for h in range(q.shape[0]):
+        s = sc * q[h] @ k[h].T
+        if causal:
+            s = np.where(np.tril(np.ones(s.shape, dtype=bool)), s, -np.inf)
+        p = np.exp(s - m[h][:, None]) / l[h][:, None]
+        dp = do[h] @ v[h].T
+        dr = (p * dp).sum(axis=1, keepdims=True)
+        a = p * (np.abs(dp) + np.abs(dr))
+        fl = np.maximum(fl, [sc * (a @ np.abs(k[h])).max(), sc * (a.T @ np.abs(q[h])).max(),
+                             (p.T @ np.abs(do[h])).max()])
+    return fl
+
+
+def _check(got, ref, dtype, label, floors=(0.0, 0.0, 0.0)):
     errs = {}
-    for name, g, w in zip(("dq", "dk", "dv"), got, ref):
+    for name, g, w, fl in zip(("dq", "dk", "dv"), got, ref, floors):
         assert np.isfinite(g).all(), f"{label}: {name} not finite"
-        scale = max(float(np.abs(w).max()), 1e-30)
+        scale = max(float(np.abs(w).max()), fl, 1e-30)
         bound = TOL[dtype] * scale + oracle.ulp(w, MANT[dtype]) / 2
         err = np.abs(g - w)
         worst = float((err / bound).max())
@@ -80,34 +108,34 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_bwd_small_shapes_vs_oracle(device, dtype, D, causal):
     for i, (B, H, S, label) in enumerate(SHAPES):
         tag = f"bwd {dtype} D={D} causal={causal} B{B} H{H} S{S} ({label})"
         _say(f"case {tag}")
-        got, ref = _run(B, H, S, D, dtype, causal, seed=300 + i)
-        errs = _check(got, ref, dtype, tag)
+        got, ref, fl = _run(B, H, S, D, dtype, causal, seed=300 + i)
+        errs = _check(got, ref, dtype, tag, fl)
         _say(f"  {errs}")
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
 def test_bwd_with_forward_output(device, dtype):
     """Row terms from <dout, O> instead of the extra pass over the keys."""
     for causal in (True, False):
         tag = f"bwd with O {dtype} causal={causal}"
         _say(f"case {tag}")
-        got, ref = _run(2, 2, 300, 64, dtype, causal, seed=400, with_o=True)
-        _check(got, ref, dtype, tag)
+        got, ref, fl = _run(2, 2, 300, 64, dtype, causal, seed=400, with_o=True)
+        _check(got, ref, dtype, tag, fl)
 
 
 def test_bwd_larger_heads_sampled(device):
     """S = 1024, head_dim 128, bf16: two heads against the oracle."""
     tag = "bwd bf16 B1 H4 S1024 D128"
     _say(f"case {tag}")
-    got, ref = _run(1, 4, 1024, 128, "bf16", True, seed=500, heads=[0, 3])
-    _check(got, ref, "bf16", tag)
+    got, ref, fl = _run(1, 4, 1024, 128, "bf16", True, seed=500, heads=[0, 3])
+    _check(got, ref, "bf16", tag, fl)
 
 
 def test_bwd_closed_form_constant_v(device):
@@ -139,8 +167,8 @@ def test_bwd_error_paths(device):
 
     import pmkl_amd
 
-    q = torch.zeros((1, 1, 64, 64), dtype=torch.float32, device="cuda:0")
-    m = torch.zeros((1, 1, 64), dtype=torch.float32, device="cuda:0")
+    q = torch.zeros((1, 1, 64, 64), dtype=torch.float64, device="cuda:0")
+    m = torch.zeros((1, 1, 64), dtype=torch.float64, device="cuda:0")
     with pytest.raises(Exception, match="dtype"):
         pmkl_amd.attn_bwd(q, q, q, q, m, m)
 

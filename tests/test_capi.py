@@ -145,17 +145,18 @@ def test_bwd_workspace_size_and_support():
     lib = capi.load()
     assert lib.pmkl_attn_bwd_workspace_size(4, 32, 4096) == 2 * 4 * 32 * 4096 * 4
     assert lib.pmkl_attn_bwd_workspace_size(0, 32, 4096) == 0
-    for dt in (capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
+    for dt in (capi.PMKL_DTYPE_F32, capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
         for d in (32, 64, 128):
             assert lib.pmkl_attn_bwd_supported(dt, d) == 1
         assert lib.pmkl_attn_bwd_supported(dt, 80) == 0
-    assert lib.pmkl_attn_bwd_supported(capi.PMKL_DTYPE_F32, 64) == 0
+    assert lib.pmkl_attn_bwd_supported(7, 64) == 0
 
 
 def test_bwd_error_paths():
     lib = capi.load()
     assert lib.pmkl_attn_bwd(None, None) == capi.PMKL_EINVAL
-    _expect_bwd(_bwd_args(dtype=capi.PMKL_DTYPE_F32), capi.PMKL_EUNSUPPORTED, "no device kernel")
+    _expect_bwd(_bwd_args(dtype=9, ml_dtype=9), capi.PMKL_EUNSUPPORTED, "no device kernel")
+    _expect_bwd(_bwd_args(dtype=capi.PMKL_DTYPE_F32, ml_dtype=capi.PMKL_DTYPE_BF16), capi.PMKL_EINVAL, "ml_dtype")
     _expect_bwd(_bwd_args(ml_dtype=capi.PMKL_DTYPE_F16), capi.PMKL_EINVAL, "ml_dtype")
     _expect_bwd(_bwd_args(seq_len=-1), capi.PMKL_EINVAL, "negative shape")
     _expect_bwd(_bwd_args(head_dim=96), capi.PMKL_EUNSUPPORTED, "head_dim 96")
