@@ -173,7 +173,8 @@ def test_bwd_error_paths(device):
         pmkl_amd.attn_bwd(q, q, q, q, m, m)
 
 
-def test_bwd_torch_operator_and_autograd_device(device):
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_bwd_torch_operator_and_autograd_device(device, dtype):
     """fused_self_attention_bw on ROCm tensors runs the device backward (same
     result as the C ABI call); the autograd entry's device branch, which hands
     the saved forward output to the kernel, is within the bound of the oracle."""
@@ -182,11 +183,11 @@ def test_bwd_torch_operator_and_autograd_device(device):
     import pmkl_amd
     from pmkl_amd import pmkl_pytorch_ext
     from pmkl_amd.pmkl_function import fused_self_attention
-    from pmkl_amd.workloads import small_inputs
+    from pmkl_amd.workloads import small_inputs, torch_dtype
 
     B, H, S, D = 1, 2, 300, 64
-    q, k, v = small_inputs(B, H, S, D, "bf16", seed=600)
-    do = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(601)).to(torch.bfloat16)
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=600)
+    do = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(601)).to(torch_dtype(dtype))
     qd, kd, vd, dod = (x.to("cuda:0") for x in (q, k, v, do))
     o, m, l = pmkl_pytorch_ext.fused_self_attention_fw(qd, kd, vd, True)
     a = pmkl_pytorch_ext.fused_self_attention_bw(dod, qd, kd, vd, m, l, True)
@@ -199,5 +200,7 @@ def test_bwd_torch_operator_and_autograd_device(device):
     out.backward(dod)
     torch.cuda.synchronize()
     r = lambda t: _np(t).reshape(B * H, S, D)
-    ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), _np(mm).reshape(B * H, S), _np(ll).reshape(B * H, S), causal=True)
-    _check([r(qg.grad), r(kg.grad), r(vg.grad)], ref, "bf16", "autograd device")
+    mn, ln = _np(mm).reshape(B * H, S), _np(ll).reshape(B * H, S)
+    ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), mn, ln, causal=True)
+    fl = _term_floors(r(q), r(k), r(v), r(do), mn, ln, True) if dtype == "fp32" else (0.0, 0.0, 0.0)
+    _check([r(qg.grad), r(kg.grad), r(vg.grad)], ref, dtype, f"autograd device {dtype}", fl)
