@@ -1,0 +1,60 @@
+"""Fixed-seed random sweep of the device forward and backward over shapes the
+hand-picked cases do not hit: batch, heads and sequence length drawn at
+random (S from 1 to 700, log-uniform, so that ragged tiles, single tiles and
+multi-item workgroups all occur), every head_dim and dtype, causal or not.
+Each case runs the forward against the float64 forward oracle
+(tests/parity.py bounds) and then the backward, fed with that forward's m and
+l, against the float64 backward oracle (bounds of test_attn_bwd_gpu.py).
+The case list is a pure function of the seed, so a failure names a case that
+reruns identically.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 24
+
+
+def _cases(seed=20261202, n=N_CASES):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(n):
+        S = int(np.clip(np.round(np.exp(rng.uniform(0.0, np.log(700.0)))), 1, 700))
+        out.append(dict(B=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)), S=S,
+                        D=int(rng.choice([32, 64, 128])), dtype=str(rng.choice(["bf16", "fp16", "fp32"])),
+                        causal=bool(rng.integers(0, 2)), seed=7000 + i))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: "B{B}H{H}S{S}D{D}-{dtype}-{c}".format(
+    c="causal" if c["causal"] else "full", **{k: v for k, v in c.items() if k != "causal"}))
+def test_random_shape_forward_and_backward(device, case):
+    import torch
+
+    import pmkl_amd
+    from oracle import oracle
+    from pmkl_amd.workloads import small_inputs, torch_dtype
+    from tests.parity import check_outputs
+    from tests.test_attn_bwd_gpu import _check, _np, _say, _term_floors
+
+    B, H, S, D, dtype, causal = (case[k] for k in ("B", "H", "S", "D", "dtype", "causal"))
+    tag = f"random B{B} H{H} S{S} D{D} {dtype} causal={causal} seed={case['seed']}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=case["seed"])
+    qd, kd, vd = (x.to("cuda:0") for x in (q, k, v))
+    o, m, l = pmkl_amd.attn_fwd(qd, kd, vd, is_causal=causal)
+    torch.cuda.synchronize()
+    check_outputs(q, k, v, o, m, l, dtype, causal=causal, label=tag)
+
+    rng = np.random.Generator(np.random.PCG64(case["seed"] + 17))
+    do = torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to(torch_dtype(dtype))
+    dq, dk, dv = pmkl_amd.attn_bwd(do.to("cuda:0"), qd, kd, vd, m, l, is_causal=causal)
+    torch.cuda.synchronize()
+    r = lambda t: _np(t).reshape(B * H, S, D)
+    mn, ln = _np(m).reshape(B * H, S), _np(l).reshape(B * H, S)
+    ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), mn, ln, causal=causal)
+    fl = _term_floors(r(q), r(k), r(v), r(do), mn, ln, causal) if dtype == "fp32" else (0.0, 0.0, 0.0)
+    _say(f"  {_check([r(dq), r(dk), r(dv)], ref, dtype, tag, fl)}")
