@@ -66,6 +66,12 @@ int w64_mode() {
     return v;
 }
 
+// XCD-aware work order unless PMKL_ATTN_NOXCD is set (read once).
+bool xcd_order_enabled() {
+    static const bool on = getenv("PMKL_ATTN_NOXCD") == nullptr;
+    return on;
+}
+
 // CUs of the current device (cached per device; 0 if it cannot be read).
 int cu_count() {
     static std::atomic<int> cache[64];
@@ -283,7 +289,7 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     p.scale_log2 = p.scale * 1.4426950408889634f;
     p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
     // XCD-grouped issue order needs whole head pairs (causal) or heads per XCD.
-    p.xcd_order = (a->dtype != PMKL_DTYPE_F32 && getenv("PMKL_ATTN_NOXCD") == nullptr && (B * H) % (a->is_causal ? 16 : 8) == 0) ? 1 : 0;
+    p.xcd_order = (a->dtype != PMKL_DTYPE_F32 && xcd_order_enabled() && (B * H) % (a->is_causal ? 16 : 8) == 0) ? 1 : 0;
 
     hipStream_t st = (hipStream_t)stream;
     // One workgroup per work item, except the 64-row kernel: one workgroup per
