@@ -244,6 +244,19 @@ def bench_softmax(args):
     alg_bytes = rows * n * (4 + 4)
     achieved = alg_bytes / (avg_ms / 1e3) / 1e9
     kernel = "softmax_fwd_kernel<float,float,4,4,false>"
+    # Reference point after the timed region: torch's device copy of the same
+    # bytes (rows * n fp32 read, the same written) on the same stream.
+    ycp = torch.empty_like(x)
+    for _ in range(max(args.warmup, 1)):
+        ycp.copy_(x)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        ycp.copy_(x)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    copy_ms = ev0.elapsed_time(ev1) / args.steps
+    del ycp
     cpu = None
     if not args.no_cpu:
         from oracle import oracle
@@ -276,6 +289,9 @@ def bench_softmax(args):
                      "traffic": read_traffic("", kernel, "pmc_softmax_fwd_fp32_131072x1024.txt"),
                      "kernel": kernel, "avg_launch_us": round(avg_ms * 1e3, 2)},
         "cpu_baseline": cpu,
+        "device_copy": {"what": "torch copy_ of the same bytes (the input into a new tensor), same stream, "
+                                "timed after the softmax", "ms": round(copy_ms, 4),
+                        "GB/s": round(alg_bytes / (copy_ms / 1e3) / 1e9, 1)},
     }
     print(json.dumps(line), flush=True)
 
