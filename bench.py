@@ -17,7 +17,7 @@ headline metric is quoted on.  Prints one JSON line.
              pmkl_pytorch_ext/fused_self_attention.cpp) on a bounded sample:
              one head of the same workload, timed single-threaded as written
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu] [--no-sdpa]
 """
 from __future__ import annotations
 
@@ -57,6 +57,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-sdpa", action="store_true",
+                    help="skip the torch scaled_dot_product_attention reference point")
     ap.add_argument("--op", default="fwd", choices=["fwd", "bwd", "softmax"],
                     help="fwd: the headline forward (default); bwd: the backward (pmkl_attn_bwd), "
                          "its own JSON line")
@@ -296,6 +298,31 @@ def bench_softmax(args):
     print(json.dumps(line), flush=True)
 
 
+def torch_sdpa_reference(q, k, v, flops, steps):
+    """Reference point, timed after the timed region: torch's own
+    scaled_dot_product_attention (causal, default scale 1/sqrt(D)) on the
+    same device tensors, with whichever backend torch picks on this image."""
+    import torch
+    import torch.nn.functional as F
+
+    what = "torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True), same tensors and stream"
+    try:
+        for _ in range(3):
+            F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / steps
+        return {"what": what, "ms": round(ms, 4), "TFLOP/s": round(flops / (ms / 1e3) / 1e12, 2), "steps": steps}
+    except Exception as ex:  # a missing backend is reported, not fatal
+        return {"what": what, "error": str(ex)[:200]}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -380,6 +407,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(w)
     if cpu is not None:
         cpu.pop("seconds", None)
+    sdpa = None if args.no_sdpa else torch_sdpa_reference(q, k, v, flops, min(args.steps, 20))
 
     line = {
         "metric": METRIC if w.name == "C3" else f"causal-attn TFLOP/s on 1 MI355X, {w.dtype} B{w.B} H{w.H} S{w.S} D{w.D}",
@@ -405,6 +433,7 @@ def main():
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
                      "hbm_GBs_algorithmic": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9, 1)},
         "cpu_baseline": cpu,
+        "torch_sdpa": sdpa,
         "wall_s_timed": round(wall, 4),
         "warmup_steps_run": warm_run,
     }
