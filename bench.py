@@ -138,8 +138,6 @@ def bench_bwd(args):
     from pmkl_amd.workloads import WORKLOADS, causal_flops, torch_inputs
 
     w = WORKLOADS[args.config]
-    if w.dtype == "fp32":
-        raise SystemExit("bench.py --op bwd: the device backward runs fp16 / bf16 only")
     dev = torch.device("cuda:0")
     q, k, v = torch_inputs(w, dev)
     g = torch.Generator(device="cpu").manual_seed(w.seed + 1)
@@ -195,9 +193,40 @@ def bench_bwd(args):
         "pct_of_mfma_peak": round(100.0 * flops / (ms / 1e3) / 1e12 / peak, 2),
         "with_o": {"ms_per_step": round(results[True], 4),
                    "value": round(flops / (results[True] / 1e3) / 1e12, 2)},
-        "kernels": ["attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"],
+        "kernels": ["attn_bwd_f32_dq_kernel", "attn_bwd_f32_dkdv_kernel"] if w.dtype == "fp32"
+        else ["attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"],
+        "torch_sdpa": None if args.no_sdpa else torch_sdpa_bwd_reference(q, k, v, do, flops, min(args.steps, 20)),
     }
     print(json.dumps(line), flush=True)
+
+
+def torch_sdpa_bwd_reference(q, k, v, do, flops, steps):
+    """Reference point, timed after the timed region: the backward of torch's
+    scaled_dot_product_attention (causal) on the same tensors, i.e.
+    torch.autograd.grad of its output with the forward graph kept, so only
+    the backward kernels run per step."""
+    import torch
+    import torch.nn.functional as F
+
+    what = ("backward of torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True): "
+            "torch.autograd.grad(out, (q, k, v), dout) with the forward graph kept")
+    try:
+        qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+        out = F.scaled_dot_product_attention(qg, kg, vg, is_causal=True)
+        for _ in range(3):
+            torch.autograd.grad(out, (qg, kg, vg), do, retain_graph=True)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            torch.autograd.grad(out, (qg, kg, vg), do, retain_graph=True)
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / steps
+        return {"what": what, "ms": round(ms, 4), "TFLOP/s": round(flops / (ms / 1e3) / 1e12, 2), "steps": steps}
+    except Exception as ex:  # a missing backend is reported, not fatal
+        return {"what": what, "error": str(ex)[:200]}
 
 
 SOFTMAX_ROWS, SOFTMAX_N = 131072, 1024
