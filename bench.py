@@ -17,7 +17,7 @@ headline metric is quoted on.  Prints one JSON line.
              pmkl_pytorch_ext/fused_self_attention.cpp) on a bounded sample:
              one head of the same workload, timed single-threaded as written
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu] [--no-sdpa]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu] [--sdpa]
 """
 from __future__ import annotations
 
@@ -57,8 +57,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-sdpa", action="store_true",
-                    help="skip the torch scaled_dot_product_attention reference point")
+    ap.add_argument("--sdpa", action="store_true",
+                    help="also time torch's scaled_dot_product_attention on the same tensors (reference point; "
+                         "off by default: its math fallback runs transposed bf16 batched products)")
     ap.add_argument("--op", default="fwd", choices=["fwd", "bwd", "softmax"],
                     help="fwd: the headline forward (default); bwd: the backward (pmkl_attn_bwd), "
                          "its own JSON line")
@@ -195,7 +196,7 @@ def bench_bwd(args):
                    "value": round(flops / (results[True] / 1e3) / 1e12, 2)},
         "kernels": ["attn_bwd_f32_dq_kernel", "attn_bwd_f32_dkdv_kernel"] if w.dtype == "fp32"
         else ["attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"],
-        "torch_sdpa": None if args.no_sdpa else torch_sdpa_bwd_reference(q, k, v, do, flops, min(args.steps, 20)),
+        "torch_sdpa": torch_sdpa_bwd_reference(q, k, v, do, flops, min(args.steps, 20)) if args.sdpa else None,
     }
     print(json.dumps(line), flush=True)
 
@@ -436,7 +437,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(w)
     if cpu is not None:
         cpu.pop("seconds", None)
-    sdpa = None if args.no_sdpa else torch_sdpa_reference(q, k, v, flops, min(args.steps, 20))
+    sdpa = torch_sdpa_reference(q, k, v, flops, min(args.steps, 20)) if args.sdpa else None
 
     line = {
         "metric": METRIC if w.name == "C3" else f"causal-attn TFLOP/s on 1 MI355X, {w.dtype} B{w.B} H{w.H} S{w.S} D{w.D}",
