@@ -503,15 +503,33 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(AttnParams p)
     float m_run = -INFINITY, l_run = 0.f;
     const int arow = key_of_arow(col);
 
+    // K/V tile staging: tile kt+1 is loaded into registers while tile kt is
+    // computed, and written to LDS at the top of the next iteration.
+    constexpr int NE = BN * D / kThreads;   // elements per thread per tensor
+    static_assert(BN * D % kThreads == 0, "whole tile per pass");
+    float kreg[NE], vreg[NE];
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            const int i = j * kThreads + tid;
+            const int r = i / D, c = i % D;
+            const int key = min(kt * BN + r, S - 1);
+            kreg[j] = kg[(int64_t)key * p.k_ss + c];
+            vreg[j] = vg[(int64_t)key * p.v_ss + c];
+        }
+    };
+    load_tile(0);
     for (int kt = 0; kt < nt; ++kt) {
         const int kbase = kt * BN;
-        for (int i = tid; i < BN * D; i += kThreads) {
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            const int i = j * kThreads + tid;
             const int r = i / D, c = i % D;
-            const int key = min(kbase + r, S - 1);
-            Ks[r * LD + c] = kg[(int64_t)key * p.k_ss + c];
-            Vs[r * LD + c] = vg[(int64_t)key * p.v_ss + c];
+            Ks[r * LD + c] = kreg[j];
+            Vs[r * LD + c] = vreg[j];
         }
         __syncthreads();
+        if (kt + 1 < nt) load_tile(kt + 1);
         const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
         if (wave_needed) {
             f32x16_t sacc;
