@@ -42,12 +42,21 @@ struct KernelChoice {
     int block_m;
 };
 
-int waves16() {
+// PMKL_ATTN_WAVES=4 or 8 pins the waves of the 16-bit MFMA kernel; 0 if unset.
+int waves16_env() {
     static const int w = [] {
         const char *e = getenv("PMKL_ATTN_WAVES");
-        return (e && atoi(e) == 4) ? 4 : 8;
+        return e ? (atoi(e) == 4 ? 4 : 8) : 0;
     }();
     return w;
+}
+
+// Waves of the 16-bit MFMA kernel where the 64-row kernel is not used:
+// measured per shape, 4 waves (128-row workgroups) for head_dim 64 at
+// 512 < S <= 2048, else 8.
+int waves16(int64_t D, int64_t S) {
+    if (const int e = waves16_env()) return e;
+    return (D == 64 && S > 512 && S <= 2048) ? 4 : 8;
 }
 
 template <typename T, int D, int NW>
@@ -57,7 +66,7 @@ KernelChoice pick16w(bool causal) {
             NW * 64, NW * 32};
 }
 // 64-row kernel choice: PMKL_ATTN_W64=0 never, =1 wherever it applies,
-// unset: for head_dim 64 and 128 (at 32 the 8-wave kernel is faster).
+// unset: for head_dim 128 (at 32 and 64 the 4- or 8-wave kernel is faster).
 int w64_mode() {
     static const int v = [] {
         const char *e = getenv("PMKL_ATTN_W64");
@@ -88,12 +97,12 @@ int cu_count() {
 }
 
 template <typename T, int D>
-KernelChoice pick16(bool causal, bool w64) {
+KernelChoice pick16(bool causal, bool w64, int waves) {
     if (w64)
         return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, true>
                        : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false>,
                 256, 256};
-    return waves16() == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
+    return waves == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
 }
 template <int D>
 KernelChoice pick32(bool causal) {
@@ -102,17 +111,17 @@ KernelChoice pick32(bool causal) {
             pmkl_amd::kThreads, pmkl_amd::kBlockM};
 }
 
-KernelChoice select_kernel(int32_t dt, int64_t d, bool causal, bool w64) {
+KernelChoice select_kernel(int32_t dt, int64_t d, bool causal, bool w64, int waves) {
     switch (dt) {
         case PMKL_DTYPE_BF16:
-            if (d == 32) return pick16<__bf16, 32>(causal, w64);
-            if (d == 64) return pick16<__bf16, 64>(causal, w64);
-            if (d == 128) return pick16<__bf16, 128>(causal, w64);
+            if (d == 32) return pick16<__bf16, 32>(causal, w64, waves);
+            if (d == 64) return pick16<__bf16, 64>(causal, w64, waves);
+            if (d == 128) return pick16<__bf16, 128>(causal, w64, waves);
             break;
         case PMKL_DTYPE_F16:
-            if (d == 32) return pick16<_Float16, 32>(causal, w64);
-            if (d == 64) return pick16<_Float16, 64>(causal, w64);
-            if (d == 128) return pick16<_Float16, 128>(causal, w64);
+            if (d == 32) return pick16<_Float16, 32>(causal, w64, waves);
+            if (d == 64) return pick16<_Float16, 64>(causal, w64, waves);
+            if (d == 128) return pick16<_Float16, 128>(causal, w64, waves);
             break;
         case PMKL_DTYPE_F32:
             if (d == 32) return pick32<32>(causal);
@@ -256,9 +265,9 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
         return st[2] >= 0 && ((S - 1) * st[2] + D) * (int64_t)es < (1LL << 31);
     };
     const int mode = w64_mode();
-    const bool w64 = mode != 0 && (mode == 1 || D >= 64) && a->dtype != PMKL_DTYPE_F32 && S > 128 &&
+    const bool w64 = mode != 0 && (mode == 1 || D >= 128) && a->dtype != PMKL_DTYPE_F32 && S > 128 &&
                      head_span_ok(ks) && head_span_ok(vs);
-    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64);
+    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64, waves16(D, S));
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
     const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;

@@ -153,7 +153,7 @@ def test_config_sampled_rows(device, name):
 
 
 @pytest.mark.parametrize("B,H,S,D,dtype,causal", [
-    (4, 64, 512, 64, "bf16", False),    # 512 items, XCD-grouped order
+    (4, 64, 512, 128, "bf16", False),   # 512 items, XCD-grouped order
     (2, 65, 512, 128, "fp16", True),    # 260 items: last round ragged, plain order
     (1, 256, 384, 128, "bf16", True),   # 512 items, half of the last q-tile's waves idle
 ])
@@ -169,6 +169,25 @@ def test_many_items_per_workgroup(device, B, H, S, D, dtype, causal):
     q, k, v = small_inputs(B, H, S, D, dtype, seed=7000 + H)
     o, m, l = _run_capi(q, k, v, device, causal=causal)
     rows = _sample_rows(S, 16, seed=S + H)
+    errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)
+    _say(f"{tag}: {errs}")
+
+
+@pytest.mark.parametrize("S", [513, 1000, 2048])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_head_dim64_four_wave_range(device, S, dtype, causal):
+    """head_dim 64 at 512 < S <= 2048 runs the MFMA kernel with 4-wave
+    (128-row) workgroups by default: sampled rows against the oracle."""
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+
+    B, H, D = 1, 3, 64
+    tag = f"{dtype} B{B} H{H} S{S} D{D} causal={causal}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=7100 + S)
+    o, m, l = _run_capi(q, k, v, device, causal=causal)
+    rows = _sample_rows(S, 24, seed=S)
     errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)
     _say(f"{tag}: {errs}")
 
