@@ -52,11 +52,11 @@ int waves16_env() {
 }
 
 // Waves of the 16-bit MFMA kernel where the 64-row kernel is not used:
-// measured per shape, 4 waves (128-row workgroups) for head_dim 64 at
-// 512 < S <= 2048, else 8.
-int waves16(int64_t D, int64_t S) {
+// measured per shape, 4 waves (128-row workgroups, finer causal load
+// balance) for causal head_dim 64 at 512 < S <= 2048, else 8.
+int waves16(int64_t D, int64_t S, bool causal) {
     if (const int e = waves16_env()) return e;
-    return (D == 64 && S > 512 && S <= 2048) ? 4 : 8;
+    return (causal && D == 64 && S > 512 && S <= 2048) ? 4 : 8;
 }
 
 template <typename T, int D, int NW>
@@ -267,7 +267,7 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     const int mode = w64_mode();
     const bool w64 = mode != 0 && (mode == 1 || D >= 128) && a->dtype != PMKL_DTYPE_F32 && S > 128 &&
                      head_span_ok(ks) && head_span_ok(vs);
-    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64, waves16(D, S));
+    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64, waves16(D, S, a->is_causal != 0));
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
     const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;

@@ -177,8 +177,9 @@ def test_many_items_per_workgroup(device, B, H, S, D, dtype, causal):
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("causal", [True, False])
 def test_head_dim64_four_wave_range(device, S, dtype, causal):
-    """head_dim 64 at 512 < S <= 2048 runs the MFMA kernel with 4-wave
-    (128-row) workgroups by default: sampled rows against the oracle."""
+    """head_dim 64 at 512 < S <= 2048 runs the MFMA kernel (4-wave, 128-row
+    workgroups when causal, 8-wave otherwise): sampled rows against the
+    oracle."""
     from pmkl_amd.workloads import small_inputs
     from tests.parity import check_outputs
 
