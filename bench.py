@@ -15,7 +15,8 @@ headline metric is quoted on.  Prints one JSON line.
              + WRITE_SIZE, scaled by a copy-kernel calibration), or null
   cpu_baseline  the reference's own CPU operator (oracle/_ref, compiled from
              pmkl_pytorch_ext/fused_self_attention.cpp) on a bounded sample:
-             one head of the same workload, timed single-threaded as written
+             one head per core on all usable cores at once (value), and one
+             head alone on one core (single_core), with the host CPU named
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu] [--sdpa]
 """
@@ -58,9 +59,13 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--warmup-seconds", type=float, default=WARMUP_MIN_S,
+                    help="minimum seconds of back-to-back warm-up launches (clock ramp; default 1.0). "
+                         "Counter runs (rocprofv3 --pmc serialises every dispatch) may lower it.")
     ap.add_argument("--sdpa", action="store_true",
                     help="also time torch's scaled_dot_product_attention on the same tensors (reference point; "
-                         "off by default: its math fallback runs transposed bf16 batched products)")
+                         "restricted to its flash / memory-efficient backends: the math fallback runs "
+                         "transposed bf16 batched products)")
     ap.add_argument("--op", default="fwd", choices=["fwd", "bwd", "softmax"],
                     help="fwd: the headline forward (default); bwd: the backward (pmkl_attn_bwd), "
                          "its own JSON line")
@@ -98,32 +103,109 @@ def read_traffic(config: str, kernel: str, name: str | None = None):
     return float(m.group(1)) if m else None
 
 
+def _host_cpu():
+    """Model name of the host CPU (/proc/cpuinfo), its logical CPU count and
+    the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"model": model, "nproc": os.cpu_count(), "usable_cpus": usable}
+
+
+# A GPU box gives one GPU's job a share of 16 CPUs, whatever nproc shows.
+CPU_WORKERS_MAX = 16
+CPU_WORKER_TIMEOUT_S = 240
+
+
+def _run_cpu_workers(npz: str, heads):
+    """One oracle.cpu_baseline worker per head (child processes that never
+    touch the GPU), released together once all have loaded their head.
+    Returns (per-worker seconds, wall seconds from release to the last
+    result), or None if a worker failed."""
+    import subprocess
+
+    procs = [subprocess.Popen([sys.executable, "-m", "oracle.cpu_baseline", npz, str(h)], cwd=str(ROOT),
+                              stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True) for h in heads]
+    try:
+        for p in procs:
+            if p.stdout.readline().strip() != "ready":
+                return None
+        t0 = time.perf_counter()
+        for p in procs:
+            p.stdin.write("go\n")
+            p.stdin.flush()
+        secs = []
+        for p in procs:
+            r = json.loads(p.stdout.readline())
+            if "seconds" not in r:
+                return None
+            secs.append(r["seconds"])
+        wall = time.perf_counter() - t0
+        for p in procs:
+            p.wait(timeout=CPU_WORKER_TIMEOUT_S)
+        return secs, wall
+    except (ValueError, OSError):
+        return None
+    finally:
+        for p in procs:
+            if p.poll() is None:
+                p.kill()
+                p.wait()
+
+
 def cpu_baseline(w):
-    """Reference CPU operator on one head of the workload (bounded sample)."""
-    import torch
+    """The reference's own CPU operator (oracle/_ref) on a bounded sample of
+    the workload: one head on one core (the operator as written walks heads
+    on one thread), then one head per core on all usable cores at once (up to
+    CPU_WORKERS_MAX), each worker on its own head.  `value` is the all-cores
+    throughput, the single-core one is reported beside it; both count the
+    same causal FLOPs as the GPU line."""
+    import tempfile
+
+    import numpy as np
 
     from oracle import oracle
-    from pmkl_amd.workloads import causal_flops, host_inputs, torch_dtype
+    from pmkl_amd.workloads import causal_flops, host_inputs
 
-    ref = oracle.reference_op()
-    if ref is None:
+    if oracle.reference_op() is None:
         return None
-    q, k, v = host_inputs(w)
-    dt = torch_dtype(w.dtype)
-    sample = [torch.from_numpy(a[:1, :1].copy()).to(dt) for a in (q, k, v)]
-    torch.set_num_threads(1)
-    t0 = time.perf_counter()
-    ref.fused_self_attention_fw(sample[0], sample[1], sample[2], True)
-    dt_s = time.perf_counter() - t0
-    flops = causal_flops(1, 1, w.S, w.D)
+    host = _host_cpu()
+    n = max(1, min(CPU_WORKERS_MAX, host["usable_cpus"], w.B * w.H))
+    q, k, v = (a.reshape(w.B * w.H, w.S, w.D)[:n] for a in host_inputs(w))
+    flops_head = causal_flops(1, 1, w.S, w.D)
+    with tempfile.TemporaryDirectory() as tmp:
+        npz = os.path.join(tmp, "heads.npz")
+        np.savez(npz, q=q, k=k, v=v, dtype=np.array(w.dtype), causal=np.array(True))
+        one = _run_cpu_workers(npz, [0])
+        many = _run_cpu_workers(npz, list(range(n)))
+    if one is None or many is None:
+        return None
+    single_s = one[0][0]
+    secs, wall = many
     return {
-        "value": flops / dt_s / 1e12,
+        "value": flops_head * n / wall / 1e12,
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": n,
         "kind": "reference",
-        "sample": f"1 of {w.B * w.H} heads of {w.name} (S={w.S}, D={w.D}, {w.dtype}, causal) through the "
-                  f"reference fused_self_attention_fw CPU body, single-threaded as written; {dt_s:.1f} s",
-        "seconds": dt_s,
+        "sample": f"{n} of {w.B * w.H} heads of {w.name} (S={w.S}, D={w.D}, {w.dtype}, causal), one head per "
+                  f"process on {n} cores at once, through the reference fused_self_attention_fw CPU body "
+                  f"(single-threaded per head as written); {wall:.3g} s wall (slowest head {max(secs):.3g} s, "
+                  f"fastest {min(secs):.3g} s)",
+        "single_core": {"value": flops_head / single_s / 1e12, "cores": 1, "seconds": float(f"{single_s:.4g}"),
+                        "sample": f"head 0 of {w.name} alone on one core"},
+        "host_cpu": host,
+        "full_job_seconds_extrapolated": {"single_core": round(single_s * w.B * w.H, 1),
+                                          "all_cores": round(wall * w.B * w.H / n, 1)},
     }
 
 
@@ -164,7 +246,7 @@ def bench_bwd(args):
                 raise capi.PmklError(rc, capi.last_error())
 
         t_w = time.perf_counter()
-        while time.perf_counter() - t_w < WARMUP_MIN_S:
+        while time.perf_counter() - t_w < args.warmup_seconds:
             for _ in range(max(args.warmup, 1)):
                 step()
             torch.cuda.synchronize()
@@ -202,6 +284,17 @@ def bench_bwd(args):
     print(json.dumps(line), flush=True)
 
 
+def _sdpa_fused_backends_only():
+    """Context that lets torch's scaled_dot_product_attention pick only its
+    flash or memory-efficient backend.  Its math fallback runs batched bf16
+    products on transposed views, which have faulted these GPU boxes; with
+    this context a missing fused backend raises (and is reported in the
+    line) instead of falling back."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    return sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION])
+
+
 def torch_sdpa_bwd_reference(q, k, v, do, flops, steps):
     """Reference point, timed after the timed region: the backward of torch's
     scaled_dot_product_attention (causal) on the same tensors, i.e.
@@ -214,7 +307,8 @@ def torch_sdpa_bwd_reference(q, k, v, do, flops, steps):
             "torch.autograd.grad(out, (q, k, v), dout) with the forward graph kept")
     try:
         qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
-        out = F.scaled_dot_product_attention(qg, kg, vg, is_causal=True)
+        with _sdpa_fused_backends_only():
+            out = F.scaled_dot_product_attention(qg, kg, vg, is_causal=True)
         for _ in range(3):
             torch.autograd.grad(out, (qg, kg, vg), do, retain_graph=True)
         torch.cuda.synchronize()
@@ -261,7 +355,7 @@ def bench_softmax(args):
             raise capi.PmklError(rc, capi.last_error())
 
     t_w = time.perf_counter()
-    while time.perf_counter() - t_w < WARMUP_MIN_S:
+    while time.perf_counter() - t_w < args.warmup_seconds:
         for _ in range(max(args.warmup, 1)):
             step()
         torch.cuda.synchronize()
@@ -338,15 +432,16 @@ def torch_sdpa_reference(q, k, v, flops, steps):
 
     what = "torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True), same tensors and stream"
     try:
-        for _ in range(3):
-            F.scaled_dot_product_attention(q, k, v, is_causal=True)
-        torch.cuda.synchronize()
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record()
-        for _ in range(steps):
-            F.scaled_dot_product_attention(q, k, v, is_causal=True)
-        ev1.record()
+        with _sdpa_fused_backends_only():
+            for _ in range(3):
+                F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            torch.cuda.synchronize()
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            for _ in range(steps):
+                F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            ev1.record()
         torch.cuda.synchronize()
         ms = ev0.elapsed_time(ev1) / steps
         return {"what": what, "ms": round(ms, 4), "TFLOP/s": round(flops / (ms / 1e3) / 1e12, 2), "steps": steps}
@@ -404,7 +499,7 @@ def main():
     # clocks ramp: at C3 the first launches take 640-830 us, then 590-600 us).
     t_w = time.perf_counter()
     warm_run = 0
-    while warm_run < args.warmup or time.perf_counter() - t_w < WARMUP_MIN_S:
+    while warm_run < args.warmup or time.perf_counter() - t_w < args.warmup_seconds:
         for _ in range(max(args.warmup, 1)):
             step()
         warm_run += max(args.warmup, 1)
@@ -436,8 +531,6 @@ def main():
     traffic = read_traffic(w.name, kernel_name(w))
 
     cpu = None if args.no_cpu else cpu_baseline(w)
-    if cpu is not None:
-        cpu.pop("seconds", None)
     sdpa = torch_sdpa_reference(q, k, v, flops, min(args.steps, 20)) if args.sdpa else None
 
     line = {

@@ -30,14 +30,48 @@ def torch_dtype_to_pmkl(dt) -> int:
     return table[dt]
 
 
+def _check_fwd_buffers(q, out, out_m, out_l, ml_dtype):
+    """Validates caller-provided output buffers of attn_fwd against q and
+    returns the dtype of m and l.  out: [B, H, S, D] in q's dtype on q's
+    device with head_dim contiguous (other strides are passed to the kernel);
+    out_m / out_l: contiguous [B, H, S] on q's device, both in one dtype,
+    which is the m/l dtype (it must agree with ml_dtype when both are given;
+    with neither, q's dtype).  The kernels write these buffers assuming
+    exactly that, so anything else raises ValueError before a launch."""
+    import torch
+
+    B, H, S, D = q.shape
+    if out is not None:
+        if tuple(out.shape) != (B, H, S, D) or out.dtype != q.dtype or out.device != q.device:
+            raise ValueError(f"out must be a [{B}, {H}, {S}, {D}] {q.dtype} tensor on {q.device}")
+        if out.stride(3) != 1:
+            raise ValueError("out: head_dim must be contiguous")
+    mdt = ml_dtype
+    for name, t in (("out_m", out_m), ("out_l", out_l)):
+        if t is None:
+            continue
+        if tuple(t.shape) != (B, H, S) or t.device != q.device or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous [{B}, {H}, {S}] tensor on {q.device}")
+        if mdt is None:
+            mdt = t.dtype
+        elif t.dtype != mdt:
+            raise ValueError(f"{name} is {t.dtype}, but the m/l dtype is {mdt}")
+    if mdt is None:
+        mdt = q.dtype
+    if mdt not in (q.dtype, torch.float32):
+        raise ValueError(f"m/l dtype must be q's dtype ({q.dtype}) or float32, got {mdt}")
+    return mdt
+
+
 def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dtype=None,
              out=None, out_m=None, out_l=None, stream=None):
     """Fused attention forward on ROCm tensors [B, H, S, D] through pmkl_attn_fwd.
 
     Returns (out, out_m, out_l).  out is contiguous [B, H, S, D] in q's dtype;
-    out_m / out_l are [B, H, S] in `ml_dtype` (default: q's dtype, as the
-    reference operator).  q, k, v may be strided as long as head_dim is
-    contiguous.  Runs on `stream` (a raw hipStream_t int) or torch's current
+    out_m / out_l are [B, H, S] in `ml_dtype` (default: the dtype of a given
+    out_m / out_l, else q's dtype, as the reference operator).  q, k, v and
+    out may be strided as long as head_dim is contiguous; given buffers are
+    validated first (_check_fwd_buffers).  Runs on `stream` (a raw hipStream_t int) or torch's current
     stream; nothing is synchronised.
     """
     import torch
@@ -48,7 +82,7 @@ def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dty
         raise ValueError("q, k, v must share a 4-D shape [B, H, S, D]")
     B, H, S, D = q.shape
     dt = torch_dtype_to_pmkl(q.dtype)
-    mdt = q.dtype if ml_dtype is None else ml_dtype
+    mdt = _check_fwd_buffers(q, out, out_m, out_l, ml_dtype)
     if out is None:
         out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
     if out_m is None:

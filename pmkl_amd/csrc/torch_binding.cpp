@@ -237,6 +237,12 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_bw(const at:
     TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type() &&
                     q.scalar_type() == dout.scalar_type(),
                 "Input tensor dtypes must match");
+    // Every tensor on q's device before anything is dispatched: a host
+    // pointer handed to a kernel (or a device pointer to the CPU body) would
+    // be dereferenced on the wrong side.
+    TORCH_CHECK(dout.device() == q.device() && k.device() == q.device() && v.device() == q.device() &&
+                    out_m.device() == q.device() && out_l.device() == q.device(),
+                "Input tensors must be on one device");
 
     auto dq = at::zeros_like(q);
     auto dk = at::zeros_like(k);

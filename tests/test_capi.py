@@ -234,3 +234,36 @@ def test_softmax_empty_problem_returns_ok_without_touching_pointers():
     assert lib.pmkl_warp_softmax_forward(0, 0, 0, None, None, 0, 0, 5, None) == capi.PMKL_OK
     assert lib.pmkl_warp_softmax_forward(0, 0, 0, None, None, 1025, 1025, 5, None) == capi.PMKL_EINVAL
     assert "softmax_elements" in capi.last_error()
+
+
+def test_attn_fwd_rejects_bad_output_buffers():
+    """Caller-provided out / out_m / out_l are validated before any launch
+    (pmkl_amd._check_fwd_buffers, run here on CPU tensors)."""
+    import torch
+
+    from pmkl_amd import _check_fwd_buffers
+
+    q = torch.empty(2, 3, 40, 64, dtype=torch.bfloat16)
+    ok_o = torch.empty_like(q)
+    ok_m = torch.empty(2, 3, 40, dtype=torch.bfloat16)
+    assert _check_fwd_buffers(q, ok_o, ok_m, ok_m.clone(), None) == torch.bfloat16
+    assert _check_fwd_buffers(q, None, None, None, None) == torch.bfloat16
+    assert _check_fwd_buffers(q, None, None, None, torch.float32) == torch.float32
+    m32 = ok_m.float()
+    assert _check_fwd_buffers(q, None, m32, m32.clone(), None) == torch.float32   # dtype taken from out_m
+    # strided out with head_dim contiguous is fine ([B, S, H, D] memory)
+    assert _check_fwd_buffers(q, torch.empty(2, 40, 3, 64, dtype=q.dtype).transpose(1, 2), None, None, None)
+    bad = [
+        ((torch.empty(2, 3, 41, 64, dtype=q.dtype), None, None, None), "out must be"),
+        ((torch.empty_like(q, dtype=torch.float16), None, None, None), "out must be"),
+        ((torch.empty(2, 3, 64, 40, dtype=q.dtype).transpose(2, 3), None, None, None), "head_dim must be contiguous"),
+        ((None, torch.empty(2, 3, 39, dtype=q.dtype), None, None), "out_m must be"),
+        ((None, None, torch.empty(2, 40, 3, dtype=q.dtype).transpose(1, 2), None), "out_l must be"),
+        ((None, ok_m, m32, None), "out_l is torch.float32"),
+        ((None, ok_m, None, torch.float32), "out_m is torch.bfloat16"),
+        ((None, torch.empty(2, 3, 40, dtype=torch.float16), None, None), "m/l dtype must be"),
+        ((None, torch.empty(2, 3, 40, dtype=q.dtype, device="meta"), None, None), "out_m must be"),
+    ]
+    for (o, m, l, mdt), msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            _check_fwd_buffers(q, o, m, l, mdt)

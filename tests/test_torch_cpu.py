@@ -148,3 +148,17 @@ def test_backward_checks_match_reference_messages():
         pmkl_pytorch_ext.fused_self_attention_bw(x, x.transpose(2, 3), x, x, m, m, True)
     with pytest.raises(RuntimeError, match="Input tensor shapes must match"):
         pmkl_pytorch_ext.fused_self_attention_bw(x, x, x[:, :1].contiguous(), x, m, m, True)
+
+
+def test_backward_rejects_tensors_on_another_device():
+    """Every tensor must sit on q's device: checked before any dispatch, so a
+    host pointer never reaches a kernel (and no device pointer the CPU body).
+    The meta device stands in for "another device" here (no GPU needed)."""
+    x = torch.randn(1, 2, 8, 32)
+    m = torch.randn(1, 2, 8)
+    xm = torch.empty_like(x, device="meta")
+    mm = torch.empty_like(m, device="meta")
+    for args in ((xm, x, x, x, m, m), (x, x, xm, x, m, m), (x, x, x, xm, m, m),
+                 (x, x, x, x, mm, m), (x, x, x, x, m, mm)):
+        with pytest.raises(RuntimeError, match="on one device"):
+            pmkl_pytorch_ext.fused_self_attention_bw(*args, True)
