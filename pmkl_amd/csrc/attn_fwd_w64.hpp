@@ -480,9 +480,13 @@ void attn_fwd_w64_kernel(AttnParams p) {
             pe[i & 1][kind] = fast_exp2(__builtin_fmaf(sc[SET][qb][kb][r + kind], p.scale_log2, moff[qb]));
             asm volatile("" : "+v"(pe[i & 1][kind]));
         } else {
-            pk[qb][kb][r >> 1] = E::pack2(pe[i & 1][0], pe[i & 1][1]);
-            l_a[qb] += pe[i & 1][0];
-            l_b[qb] += pe[i & 1][1];
+            // The row sums take the probabilities as rounded for the PV
+            // product, so O is normalised by exactly the weights it was
+            // built from.
+            const uint32_t w = E::pack2(pe[i & 1][0], pe[i & 1][1]);
+            pk[qb][kb][r >> 1] = w;
+            l_a[qb] = E::add_lo(w, l_a[qb]);
+            l_b[qb] = E::add_hi(w, l_b[qb]);
             asm volatile("" : "+v"(pk[qb][kb][r >> 1]), "+v"(l_a[qb]), "+v"(l_b[qb]));
         }
     };
