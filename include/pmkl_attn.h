@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define PMKL_ABI_VERSION 2
+#define PMKL_ABI_VERSION 3
 
 /* Element types.  The reference dispatches on float, double, half and
  * bfloat16 (fused_self_attention.cpp:152-156); the device path implements
@@ -147,6 +147,24 @@ int pmkl_attn_bwd(const pmkl_attn_bwd_args *args, void *stream);
 
 /* 1 if a backward kernel is compiled for (dtype, head_dim), else 0. */
 int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim);
+
+/* Largest batch * heads * seq_len that pmkl_attn_bwd_noalloc accepts. */
+#define PMKL_ATTN_BWD_NOALLOC_MAX_ROWS 1048576
+
+/* pmkl_attn_bwd without a caller workspace, and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The two floats per query row that pmkl_attn_bwd
+ * keeps in args->workspace live instead in a fixed 8 MiB device array of the
+ * library (one per GPU, held until the process ends), so batch * heads *
+ * seq_len must not exceed PMKL_ATTN_BWD_NOALLOC_MAX_ROWS (else PMKL_EINVAL,
+ * nothing launched).  args->workspace and args->workspace_bytes are ignored;
+ * everything else is as for pmkl_attn_bwd, with identical results.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.  The
+ * first call on a device looks up the array's device address (no allocation).
+ * ABI version 3. */
+int pmkl_attn_bwd_noalloc(const pmkl_attn_bwd_args *args, void *stream);
 
 /* Thread-local text of the last error ("" if none), with the file:line of the
  * check that failed, in the style of the reference's CHECK_FAIL message. */

@@ -22,6 +22,7 @@ PMKL_EUNSUPPORTED = 2
 PMKL_EHIP = 3
 
 PMKL_SOFTMAX_MAX_ELEMENTS = 1024
+PMKL_ATTN_BWD_NOALLOC_MAX_ROWS = 1048576   # include/pmkl_attn.h
 
 # Every symbol include/pmkl_attn.h and include/pmkl_softmax.h declare.
 EXPORTED_SYMBOLS = (
@@ -31,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "pmkl_attn_bwd_workspace_size",
     "pmkl_attn_bwd",
     "pmkl_attn_bwd_supported",
+    "pmkl_attn_bwd_noalloc",
     "pmkl_last_error",
     "pmkl_abi_version",
     "pmkl_softmax_fwd",
@@ -140,6 +142,8 @@ def load() -> ctypes.CDLL:
     lib.pmkl_attn_bwd_workspace_size.restype = ctypes.c_uint64
     lib.pmkl_attn_bwd.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_void_p]
     lib.pmkl_attn_bwd.restype = ctypes.c_int
+    lib.pmkl_attn_bwd_noalloc.argtypes = [ctypes.POINTER(AttnBwdArgs), ctypes.c_void_p]
+    lib.pmkl_attn_bwd_noalloc.restype = ctypes.c_int
     lib.pmkl_attn_bwd_supported.argtypes = [ctypes.c_int32, ctypes.c_int64]
     lib.pmkl_attn_bwd_supported.restype = ctypes.c_int
     lib.pmkl_softmax_fwd.argtypes = [ctypes.POINTER(SoftmaxArgs), ctypes.c_void_p]
@@ -187,6 +191,12 @@ def make_args(q, k, v, o, m, l, *, dtype: int, ml_dtype: int | None = None, batc
 def attn_bwd_raw(args: AttnBwdArgs, stream: int | None = None) -> int:
     """Call pmkl_attn_bwd; returns the status code."""
     return load().pmkl_attn_bwd(ctypes.byref(args), ctypes.c_void_p(stream or 0))
+
+
+def attn_bwd_noalloc_raw(args: AttnBwdArgs, stream: int | None = None) -> int:
+    """Call pmkl_attn_bwd_noalloc (the workspace fields of args are ignored);
+    returns the status code."""
+    return load().pmkl_attn_bwd_noalloc(ctypes.byref(args), ctypes.c_void_p(stream or 0))
 
 
 def make_bwd_args(dout, q, k, v, o, m, l, dq, dk, dv, workspace, workspace_bytes, *, dtype: int,

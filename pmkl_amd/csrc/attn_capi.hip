@@ -215,6 +215,125 @@ BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
     return {nullptr, nullptr, 0, 0, 0, 0, false};
 }
 
+// Validates a backward call except for the workspace.  *empty is set for a
+// problem with no rows (nothing to launch).
+int check_bwd(const pmkl_attn_bwd_args *a, bool *empty) {
+    PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
+    PMKL_REQUIRE(dtype_valid(a->dtype), PMKL_EUNSUPPORTED,
+                 "backward dtype %d has no device kernel (supported: F32, F16, BF16)", (int)a->dtype);
+    PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
+                 "ml_dtype %d must equal dtype %d or be F32", (int)a->ml_dtype, (int)a->dtype);
+    PMKL_REQUIRE(a->batch >= 0 && a->heads >= 0 && a->seq_len >= 0, PMKL_EINVAL,
+                 "negative shape (batch %lld, heads %lld, seq %lld)", (long long)a->batch, (long long)a->heads,
+                 (long long)a->seq_len);
+    PMKL_REQUIRE(head_dim_supported(a->head_dim), PMKL_EUNSUPPORTED,
+                 "head_dim %lld has no compiled kernel (supported: 32, 64, 128)", (long long)a->head_dim);
+    PMKL_REQUIRE(std::isfinite(a->scale) && a->scale >= 0.f, PMKL_EINVAL, "scale must be finite and >= 0");
+    *empty = a->batch * a->heads * a->seq_len == 0;
+    if (*empty) return PMKL_OK;
+
+    const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
+    PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
+                 (long long)(B * H), (long long)S);
+    PMKL_REQUIRE(B * H * S * D < (1LL << 62), PMKL_EINVAL, "tensors span too many elements");
+    const struct {
+        const char *name;
+        const void *ptr;
+    } tensors[] = {{"dout", a->dout}, {"q", a->q}, {"k", a->k}, {"v", a->v}, {"dq", a->dq}, {"dk", a->dk},
+                   {"dv", a->dv}};
+    for (const auto &t : tensors) {
+        PMKL_REQUIRE(t.ptr != nullptr, PMKL_EINVAL, "%s is a null pointer", t.name);
+        PMKL_REQUIRE(((uintptr_t)t.ptr % 16) == 0, PMKL_EINVAL, "%s must be 16-byte aligned", t.name);
+    }
+    PMKL_REQUIRE(a->o == nullptr || ((uintptr_t)a->o % 16) == 0, PMKL_EINVAL, "o must be 16-byte aligned");
+    PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
+    const size_t ml_es = dtype_size(a->ml_dtype);
+    PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
+                 "m / l must be aligned to their element size");
+    const BwdKernels kc = select_bwd(a->dtype, D, a->is_causal != 0);
+    PMKL_REQUIRE(kc.dq != nullptr, PMKL_EUNSUPPORTED, "no backward kernel for dtype %d head_dim %lld",
+                 (int)a->dtype, (long long)D);
+    const int64_t nq = (S + kc.dq_rows - 1) / kc.dq_rows, nk = (S + kc.dkdv_rows - 1) / kc.dkdv_rows;
+    const int64_t gq = kc.flat ? (B * H * S + kc.dq_rows - 1) / kc.dq_rows : nq * B * H;
+    const int64_t gk = kc.flat ? (B * H * S + kc.dkdv_rows - 1) / kc.dkdv_rows : nk * B * H;
+    PMKL_REQUIRE(std::max(gq, gk) <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
+                 (long long)std::max(gq, gk));
+    return PMKL_OK;
+}
+
+// Launches the two backward passes of a validated, non-empty call.  ws holds
+// two floats per query row (log2-sum-exp, then sum_j P dP): the dq pass writes
+// every row's pair before the dk/dv pass, on the same stream, reads it, so
+// nothing in it needs clearing.
+int launch_bwd(const pmkl_attn_bwd_args *a, float *ws, void *stream) {
+    const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
+    const BwdKernels kc = select_bwd(a->dtype, D, a->is_causal != 0);
+    const int64_t nq = (S + kc.dq_rows - 1) / kc.dq_rows, nk = (S + kc.dkdv_rows - 1) / kc.dkdv_rows;
+    const int64_t gq = kc.flat ? (B * H * S + kc.dq_rows - 1) / kc.dq_rows : nq * B * H;
+    const int64_t gk = kc.flat ? (B * H * S + kc.dkdv_rows - 1) / kc.dkdv_rows : nk * B * H;
+
+    BwdParams p;
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.dout = a->dout;
+    p.m = a->m;
+    p.l = a->l;
+    p.dq = a->dq;
+    p.dk = a->dk;
+    p.dv = a->dv;
+    p.lse2 = ws;
+    p.drow = ws + B * H * S;
+    p.S = (int32_t)S;
+    p.BH = (int32_t)(B * H);
+    p.n_qtiles = (int32_t)nq;
+    p.n_ktiles = (int32_t)nk;
+    p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
+    p.scale_log2 = p.scale * 1.4426950408889634f;
+    p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
+
+    hipStream_t st = (hipStream_t)stream;
+    // dQ first: it writes the row vectors the dK/dV pass reads.
+    hipLaunchKernelGGL(kc.dq, dim3((unsigned)gq), dim3(kc.dq_threads), 0, st, p);
+    hipError_t err = hipGetLastError();
+    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dq kernel launch failed: %s", hipGetErrorString(err));
+    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)gk), dim3(kc.dkdv_threads), 0, st, p);
+    err = hipGetLastError();
+    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dk/dv kernel launch failed: %s", hipGetErrorString(err));
+    return PMKL_OK;
+}
+
+// Workspace of pmkl_attn_bwd_noalloc: two floats per query row for up to
+// PMKL_ATTN_BWD_NOALLOC_MAX_ROWS rows (8 MiB), static device memory of this
+// code object, so each GPU the library runs on holds its own copy until the
+// process ends.  In host code `scratch` only names the symbol; its device
+// address comes from hipGetSymbolAddress (scratch_on_device), never from the
+// name itself.
+static __device__ __align__(256) float scratch[2 * PMKL_ATTN_BWD_NOALLOC_MAX_ROWS];
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device (with that device current) and cached per device.
+int scratch_on_device(float **out) {
+    static std::atomic<void *> cache[64];
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    PMKL_REQUIRE(err == hipSuccess && dev >= 0, PMKL_EHIP, "hipGetDevice failed: %s", hipGetErrorString(err));
+    if (dev < 64) {
+        if (void *p = cache[dev].load(std::memory_order_acquire)) {
+            *out = (float *)p;
+            return PMKL_OK;
+        }
+    }
+    void *ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    PMKL_REQUIRE(err == hipSuccess && ptr != nullptr, PMKL_EHIP, "hipGetSymbolAddress(scratch) failed: %s",
+                 hipGetErrorString(err));
+    if (dev < 64) cache[dev].store(ptr, std::memory_order_release);
+    *out = (float *)ptr;
+    return PMKL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -326,83 +445,29 @@ int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim) {
 
 int pmkl_attn_bwd(const pmkl_attn_bwd_args *a, void *stream) {
     pmkl_capi::g_err[0] = '\0';
-    PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
-    PMKL_REQUIRE(dtype_valid(a->dtype), PMKL_EUNSUPPORTED,
-                 "backward dtype %d has no device kernel (supported: F32, F16, BF16)", (int)a->dtype);
-    PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
-                 "ml_dtype %d must equal dtype %d or be F32", (int)a->ml_dtype, (int)a->dtype);
-    PMKL_REQUIRE(a->batch >= 0 && a->heads >= 0 && a->seq_len >= 0, PMKL_EINVAL,
-                 "negative shape (batch %lld, heads %lld, seq %lld)", (long long)a->batch, (long long)a->heads,
-                 (long long)a->seq_len);
-    PMKL_REQUIRE(head_dim_supported(a->head_dim), PMKL_EUNSUPPORTED,
-                 "head_dim %lld has no compiled kernel (supported: 32, 64, 128)", (long long)a->head_dim);
-    PMKL_REQUIRE(std::isfinite(a->scale) && a->scale >= 0.f, PMKL_EINVAL, "scale must be finite and >= 0");
-    if (a->batch * a->heads * a->seq_len == 0) return PMKL_OK;
-
-    const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
-    PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
-                 (long long)(B * H), (long long)S);
-    PMKL_REQUIRE(B * H * S * D < (1LL << 62), PMKL_EINVAL, "tensors span too many elements");
-    const struct {
-        const char *name;
-        const void *ptr;
-    } tensors[] = {{"dout", a->dout}, {"q", a->q}, {"k", a->k}, {"v", a->v}, {"dq", a->dq}, {"dk", a->dk},
-                   {"dv", a->dv}};
-    for (const auto &t : tensors) {
-        PMKL_REQUIRE(t.ptr != nullptr, PMKL_EINVAL, "%s is a null pointer", t.name);
-        PMKL_REQUIRE(((uintptr_t)t.ptr % 16) == 0, PMKL_EINVAL, "%s must be 16-byte aligned", t.name);
-    }
-    PMKL_REQUIRE(a->o == nullptr || ((uintptr_t)a->o % 16) == 0, PMKL_EINVAL, "o must be 16-byte aligned");
-    PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
-    const size_t ml_es = dtype_size(a->ml_dtype);
-    PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
-                 "m / l must be aligned to their element size");
-    const uint64_t ws = pmkl_attn_bwd_workspace_size(B, H, S);
+    bool empty = false;
+    int rc = check_bwd(a, &empty);
+    if (rc != PMKL_OK || empty) return rc;
+    const uint64_t ws = pmkl_attn_bwd_workspace_size(a->batch, a->heads, a->seq_len);
     PMKL_REQUIRE(a->workspace != nullptr && ((uintptr_t)a->workspace % 16) == 0, PMKL_EINVAL,
                  "workspace must be a 16-byte aligned device pointer");
     PMKL_REQUIRE(a->workspace_bytes >= ws, PMKL_EINVAL, "workspace of %llu bytes is too small (needs %llu)",
                  (unsigned long long)a->workspace_bytes, (unsigned long long)ws);
+    return launch_bwd(a, (float *)a->workspace, stream);
+}
 
-    const BwdKernels kc = select_bwd(a->dtype, D, a->is_causal != 0);
-    PMKL_REQUIRE(kc.dq != nullptr, PMKL_EUNSUPPORTED, "no backward kernel for dtype %d head_dim %lld",
-                 (int)a->dtype, (long long)D);
-    const int64_t nq = (S + kc.dq_rows - 1) / kc.dq_rows, nk = (S + kc.dkdv_rows - 1) / kc.dkdv_rows;
-    // workgroups of each kernel
-    const int64_t gq = kc.flat ? (B * H * S + kc.dq_rows - 1) / kc.dq_rows : nq * B * H;
-    const int64_t gk = kc.flat ? (B * H * S + kc.dkdv_rows - 1) / kc.dkdv_rows : nk * B * H;
-    PMKL_REQUIRE(std::max(gq, gk) <= 0x7fffffffLL, PMKL_EINVAL, "grid too large (%lld workgroups)",
-                 (long long)std::max(gq, gk));
-
-    BwdParams p;
-    p.q = a->q;
-    p.k = a->k;
-    p.v = a->v;
-    p.o = a->o;
-    p.dout = a->dout;
-    p.m = a->m;
-    p.l = a->l;
-    p.dq = a->dq;
-    p.dk = a->dk;
-    p.dv = a->dv;
-    p.lse2 = (float *)a->workspace;
-    p.drow = (float *)a->workspace + B * H * S;
-    p.S = (int32_t)S;
-    p.BH = (int32_t)(B * H);
-    p.n_qtiles = (int32_t)nq;
-    p.n_ktiles = (int32_t)nk;
-    p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
-    p.scale_log2 = p.scale * 1.4426950408889634f;
-    p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
-
-    hipStream_t st = (hipStream_t)stream;
-    // dQ first: it writes the row vectors the dK/dV pass reads.
-    hipLaunchKernelGGL(kc.dq, dim3((unsigned)gq), dim3(kc.dq_threads), 0, st, p);
-    hipError_t err = hipGetLastError();
-    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dq kernel launch failed: %s", hipGetErrorString(err));
-    hipLaunchKernelGGL(kc.dkdv, dim3((unsigned)gk), dim3(kc.dkdv_threads), 0, st, p);
-    err = hipGetLastError();
-    PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "dk/dv kernel launch failed: %s", hipGetErrorString(err));
-    return PMKL_OK;
+int pmkl_attn_bwd_noalloc(const pmkl_attn_bwd_args *a, void *stream) {
+    pmkl_capi::g_err[0] = '\0';
+    bool empty = false;
+    int rc = check_bwd(a, &empty);
+    if (rc != PMKL_OK || empty) return rc;
+    const int64_t rows = a->batch * a->heads * a->seq_len;
+    PMKL_REQUIRE(rows <= PMKL_ATTN_BWD_NOALLOC_MAX_ROWS, PMKL_EINVAL,
+                 "pmkl_attn_bwd_noalloc handles at most %d query rows (batch * heads * seq_len), got %lld; "
+                 "use pmkl_attn_bwd with a workspace", (int)PMKL_ATTN_BWD_NOALLOC_MAX_ROWS, (long long)rows);
+    float *ws = nullptr;
+    if ((rc = scratch_on_device(&ws)) != PMKL_OK) return rc;
+    return launch_bwd(a, ws, stream);
 }
 
 int pmkl_causal_attention_forward(int32_t dtype, void *out, const void *q, const void *k, const void *v,

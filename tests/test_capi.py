@@ -40,7 +40,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_abi_version_and_support_matrix():
     lib = capi.load()
-    assert lib.pmkl_abi_version() == 2
+    assert lib.pmkl_abi_version() == 3
     for dt in (capi.PMKL_DTYPE_F32, capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
         for d in (32, 64, 128):
             assert lib.pmkl_attn_fwd_supported(dt, d) == 1
