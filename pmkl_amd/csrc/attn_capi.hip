@@ -96,6 +96,24 @@ int cu_count() {
     return n;
 }
 
+// Layout of the 64-row kernel at head_dim 128: by default two waves of 32
+// rows per SIMD (8 waves per workgroup, measured 4-6% faster at C3 and equal
+// at C4); PMKL_ATTN_W32=0 keeps one wave of 64 rows per SIMD.
+int w32_mode() {
+    static const int v = [] {
+        const char *e = getenv("PMKL_ATTN_W32");
+        return e ? (atoi(e) == 0 ? 0 : 1) : 1;
+    }();
+    return v;
+}
+
+template <typename T>
+KernelChoice pick_w32(bool causal) {
+    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 128, true, 1, 8>
+                   : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 128, false, 1, 8>,
+            512, 256};
+}
+
 template <typename T, int D>
 KernelChoice pick16(bool causal, bool w64, int waves) {
     if (w64)
@@ -386,7 +404,10 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     const int mode = w64_mode();
     const bool w64 = mode != 0 && (mode == 1 || D >= 128) && a->dtype != PMKL_DTYPE_F32 && S > 128 &&
                      head_span_ok(ks) && head_span_ok(vs);
-    const KernelChoice kc = select_kernel(a->dtype, D, a->is_causal != 0, w64, waves16(D, S, a->is_causal != 0));
+    const bool w32 = w64 && D == 128 && w32_mode() == 1;
+    const bool bf = a->dtype == PMKL_DTYPE_BF16;
+    const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(a->is_causal != 0) : pick_w32<_Float16>(a->is_causal != 0))
+                                : select_kernel(a->dtype, D, a->is_causal != 0, w64, waves16(D, S, a->is_causal != 0));
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
     const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;

@@ -111,14 +111,6 @@ template <> struct Elt16<__bf16> {
         const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
         return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, packed), one, acc, false);
     }
-    // acc + the low / high element of a packed pair, each exactly as stored
-    // (a bf16 is the upper half of the float with the same value).
-    static __device__ __forceinline__ float add_lo(uint32_t packed, float acc) {
-        return acc + __uint_as_float(packed << 16);
-    }
-    static __device__ __forceinline__ float add_hi(uint32_t packed, float acc) {
-        return acc + __uint_as_float(packed & 0xffff0000u);
-    }
 };
 template <> struct Elt16<_Float16> {
     typedef f16x8_t frag;
@@ -132,19 +124,6 @@ template <> struct Elt16<_Float16> {
     static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
         const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
         return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, packed), one, acc, false);
-    }
-    // acc + the low / high element of a packed pair: one v_fma_mix_f32 each
-    // (the fp16 operand widened exactly, times 1.0, plus acc); written out
-    // because the compiler emits a separate conversion and add.
-    static __device__ __forceinline__ float add_lo(uint32_t packed, float acc) {
-        float r;
-        asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(acc));
-        return r;
-    }
-    static __device__ __forceinline__ float add_hi(uint32_t packed, float acc) {
-        float r;
-        asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(packed), "v"(acc));
-        return r;
     }
 };
 

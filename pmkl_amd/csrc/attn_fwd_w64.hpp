@@ -1,19 +1,28 @@
-// 64-rows-per-wave variant of the 16-bit attention kernel (gfx950).
+// Slot-scheduled variant of the 16-bit attention kernel (gfx950).
 //
 // Same layouts and arithmetic as attn_fwd_mfma16_kernel (transposed scores
 // S^T = K Q^T, P kept in registers as the B operand of O^T = V^T P^T, V^T from
-// ds_read_b64_tr_b16, lazy rescale).  One wave per SIMD (4 waves, 256 query
-// rows per workgroup); each wave owns two 32-row blocks, and every K or V
-// fragment it reads from LDS feeds one MFMA of each block, which halves the
-// LDS operand reads per MFMA.
+// ds_read_b64_tr_b16, lazy rescale).  256 query rows per workgroup, in one of
+// two layouts (template parameters QB, NW):
+//  * QB = 2, NW = 4: one wave per SIMD, each owning two 32-row blocks; every
+//    K or V fragment read from LDS feeds one MFMA of each block, which halves
+//    the LDS operand reads per MFMA;
+//  * QB = 1, NW = 8: two waves per SIMD, 32 rows each, both running the same
+//    schedule: when one wave waits (barrier, LDS, a dependency), the other
+//    issues.  A wave that issues an MFMA while the matrix core is busy blocks
+//    the SIMD's vector issue of the other wave too, so the waves do not split
+//    into an MFMA wave and a softmax wave: each keeps its own vector work
+//    between its own MFMAs.
 //
 // Software pipeline: iteration t issues, one MFMA per slot,
-//   slots 0 .. QKS-1       QK of tile t+1 (both blocks, score set (t+1) & 1)
-//   slots QKS .. NSLOT-1   PV of tile t   (both blocks)
+//   slots 0 .. QKS-1       QK of tile t+1 (every block, score set (t+1) & 1)
+//   slots QKS .. NSLOT-1   PV of tile t (every block), each group of PV
+//                          MFMAs followed by the row-sum MFMAs of its
+//                          probabilities (an all-ones A operand)
 // and behind every MFMA a share of the VALU work, placed at compile time
-// (W64Sched): the exponentials, packing and row sums of tile t, finished a
-// slot before the PV MFMA that reads them, then the row maxima of tile t+1
-// once its QK is done.  The wave issues in order, so what stands between two
+// (W64Sched): the exponentials and packing of tile t, finished a slot before
+// the PV MFMA that reads them, then the row maxima of tile t+1 once its QK is
+// done.  The wave issues in order, so what stands between two
 // MFMAs must fit under one MFMA (~32 clocks of the matrix core): an MFMA
 // issued straight behind another stalls the wave, and its VALU share with it.
 // sched_barrier fences pin every slot; asm-volatile register pins keep the
@@ -25,9 +34,9 @@
 // of a fragment is the same in every iteration); the last RING reads of an
 // iteration already fetch the first K fragments of the next one.
 //
-// Registers: O^T accumulators (2 x D/32 x 16) and the Q fragments live in
-// AGPRs, used only by MFMAs issued from inline asm; scores, P and operands
-// live in VGPRs.  The compiler cannot see inside those MFMAs, so the kernel
+// Registers: O^T accumulators (QB x D/32 x 16), row sums (QB x 16) and the
+// Q fragments live in AGPRs, used only by MFMAs issued from inline asm;
+// scores, P and operands live in VGPRs.  The compiler cannot see inside those MFMAs, so the kernel
 // keeps the MFMA -> VALU hazard distances itself (w64_mfma_drain before the
 // first VALU access of an MFMA result, and P written a full slot before the
 // MFMA that reads it).
@@ -108,44 +117,67 @@ __device__ __forceinline__ void w64_static_for(F &&f) {
     }
 }
 
-// Compile-time slot schedule of one iteration (head_dim D).
-template <int D> struct W64Sched {
+// Compile-time slot schedule of one iteration (head_dim D, QB 32-row query
+// blocks per wave), one MFMA per slot:
+//   slots 0 .. QKS-1      QK of tile t+1: fragment s / QB, block s % QB
+//   then 4 groups (kb, c) of GS slots: the NDB QB PV MFMAs of the group
+//   (fragment, block), then QB row-sum MFMAs (block), which add the group's
+//   packed probabilities into the row sums (all-ones A operand).
+template <int D, int QB> struct W64Sched {
     static constexpr int NDB = D / 32;            // 32-wide blocks of head_dim
     static constexpr int NDK = D / 16;            // 16-deep MFMA steps over head_dim
     static constexpr int NKF = 2 * NDK;           // K fragments per tile: (dk, kb)
     static constexpr int NVF = 4 * NDB;           // V^T fragments per tile: (kb, c, db)
     static constexpr int NF = NKF + NVF;          // fragments per iteration
-    static constexpr int NSLOT = 2 * NF;          // MFMAs per iteration
-    static constexpr int QKS = 2 * NKF;           // first PV slot
+    static constexpr int QKS = QB * NKF;          // first PV slot
+    static constexpr int GS = QB * (NDB + 1);     // slots per PV group
+    static constexpr int NSLOT = QKS + 4 * GS;    // MFMAs per iteration
     static constexpr int RING = 4;                // fragments read ahead
-    static constexpr int BARS = NSLOT - 2 * RING + 1;   // barrier slot: before the first next-tile read
+    enum { QK = 0, PV = 1, SUM = 2 };
+    static constexpr int kind(int s) { return s < QKS ? QK : (s - QKS) % GS < NDB * QB ? PV : SUM; }
+    // fragment of a QK / PV slot, block of any slot, group of a PV / SUM slot
+    static constexpr int frag_of(int s) {
+        return s < QKS ? s / QB : NKF + ((s - QKS) / GS) * NDB + ((s - QKS) % GS) / QB;
+    }
+    static constexpr int qb_of(int s) {
+        return s < QKS ? s % QB : (s - QKS) % GS < NDB * QB ? ((s - QKS) % GS) % QB : (s - QKS) % GS - NDB * QB;
+    }
+    static constexpr int group_of(int s) { return (s - QKS) / GS; }
+    // slot of fragment g's last-block MFMA, after which its ring entry is refilled
+    static constexpr int last_slot(int g) {
+        return g < NKF ? QB * g + QB - 1 : QKS + ((g - NKF) / NDB) * GS + ((g - NKF) % NDB) * QB + QB - 1;
+    }
+    // Barrier slot: the slot whose refill is the first read of a next-tile
+    // fragment (fragment NF - RING).
+    static constexpr int BARS = last_slot(NF - RING);
     static_assert(NF % RING == 0, "ring position must repeat every iteration");
 
     // Exponential pairs in the order the PV MFMAs read them: pair i covers
     // score registers 2 r2 and 2 r2 + 1 of block qb, key block kb; the PV
     // fragments (kb, c, *) read pairs 4c .. 4c+3 of (qb, kb).
-    static constexpr int pair_c(int i) { return (i >> 3) & 1; }
-    static constexpr int pair_kb(int i) { return i >> 4; }
-    static constexpr int pair_qb(int i) { return (i >> 2) & 1; }
+    static constexpr int NP = 16 * QB;            // pairs per tile
+    static constexpr int pair_c(int i) { return (i / (4 * QB)) & 1; }
+    static constexpr int pair_kb(int i) { return i / (8 * QB); }
+    static constexpr int pair_qb(int i) { return (i >> 2) % QB; }
     static constexpr int pair_r2(int i) { return 4 * pair_c(i) + (i & 3); }
-    static constexpr int pair_need(int i) { return QKS + 2 * NDB * (2 * pair_kb(i) + pair_c(i)); }
+    static constexpr int pair_need(int i) { return QKS + GS * (2 * pair_kb(i) + pair_c(i)); }
 
-    // Exponential units, three per pair: A (first exp), B (second), C (pack
-    // and row sums), in the stream A0 B0 A1 B1 C0 A2 B2 C1 ... A31 B31 C30 C31,
-    // spread evenly over slots 0 .. ES-1.
-    static constexpr int NU = 96;
-    static constexpr int ES = QKS + 6 * NDB - 1;
+    // Exponential units, three per pair: A (first exp), B (second), C
+    // (pack), in the stream A0 B0 A1 B1 C0 A2 B2 C1 ... A(NP-1) B(NP-1)
+    // C(NP-2) C(NP-1), spread evenly over slots 0 .. ES-1.
+    static constexpr int NU = 3 * NP;
+    static constexpr int ES = QKS + 3 * GS - 1;
     static constexpr int unit_slot(int n) { return n * ES / NU; }
     static constexpr int unit_first(int s) { return (s * NU + ES - 1) / ES; }   // first unit of slot s
     static constexpr int unit_kind(int n) { return n < 2 ? n : n == NU - 1 ? 2 : (n - 2) % 3; }
     static constexpr int unit_pair(int n) {
-        return n < 2 ? 0 : n == NU - 1 ? 31 : (n - 2) % 3 == 2 ? (n - 2) / 3 : (n - 2) / 3 + 1;
+        return n < 2 ? 0 : n == NU - 1 ? NP - 1 : (n - 2) % 3 == 2 ? (n - 2) / 3 : (n - 2) / 3 + 1;
     }
-    static constexpr int c_unit(int i) { return i == 31 ? NU - 1 : 3 * i + 4; }
+    static constexpr int c_unit(int i) { return i == NP - 1 ? NU - 1 : 3 * i + 4; }
 
-    // Maxima of tile t+1: drain and mask at slot MS0, then 8 partial maxima
-    // (qb, kb, half), the two block maxima and the two block updates.
-    static constexpr int NMU = 12;
+    // Maxima of tile t+1: drain and mask at slot MS0, then 4 QB partial maxima
+    // (qb, kb, half), the QB block maxima and the QB block updates.
+    static constexpr int NMU = 6 * QB;
     static constexpr int MS0 = QKS + 2;
     static constexpr int max_slot(int k) { return MS0 + k * (NSLOT - 1 - MS0) / (NMU - 1); }
 
@@ -157,32 +189,40 @@ template <int D> struct W64Sched {
             if (unit_slot(n) < 0 || unit_slot(n) >= ES || unit_first(unit_slot(n)) > n ||
                 unit_first(unit_slot(n) + 1) <= n)
                 return false;
-        for (int i = 0; i < 32; ++i)
+        for (int i = 0; i < NP; ++i)
             if (unit_slot(c_unit(i)) > pair_need(i) - 2) return false;   // P ready a slot early
         // The block updates change the exponent offsets: after every exponential.
-        if (max_slot(10) < ES) return false;
+        if (max_slot(5 * QB) < ES) return false;
         if (max_slot(NMU - 1) != NSLOT - 1) return false;
-        return BARS > QKS && BARS % 2 == 1;
+        for (int s = 0; s < NSLOT; ++s)   // slot decoding is consistent
+            if (kind(s) != SUM && last_slot(frag_of(s)) < s) return false;
+        return BARS > QKS && kind(BARS) == PV;
     }
     static_assert(valid(), "slot schedule");
 };
 
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// QB 32-row query blocks per wave, NW waves per workgroup (NW / 4 per SIMD),
+// 32 QB NW = 256 query rows per workgroup: (QB, NW) = (2, 4) is one wave of 64
+// rows per SIMD; (1, 8) two waves of 32 rows per SIMD, each running the same
+// slot schedule, so that one wave issues while the other waits.
+template <typename T, int D, bool CAUSAL, int QB = 2, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void attn_fwd_w64_kernel(AttnParams p) {
     using E = Elt16<T>;
     using M = W64Mma<T>;
-    using Sch = W64Sched<D>;
+    using Sch = W64Sched<D, QB>;
     using frag = typename E::frag;
-    constexpr int kBlockM = 256;            // query rows per workgroup (64 per wave)
+    constexpr int NT = 64 * NW;             // threads per workgroup
+    constexpr int kBlockM = 32 * QB * NW;   // query rows per workgroup
+    static_assert(kBlockM == 256, "work items are 256-row query tiles");
     constexpr int BN = 64;                  // keys per tile
     constexpr int CPR = D / 8;              // 16-byte chunks per row
     constexpr int TILE_CHUNKS = BN * CPR;   // chunks per K (or V) tile
-    constexpr int LOADS = TILE_CHUNKS / 256;   // DMAs per thread per tensor per tile
+    constexpr int LOADS = TILE_CHUNKS / NT;   // DMAs per thread per tensor per tile
     constexpr int TILE_BYTES = BN * D * (int)sizeof(T);
     constexpr int NDB = Sch::NDB, NDK = Sch::NDK, NKF = Sch::NKF, NF = Sch::NF;
     constexpr int NSLOT = Sch::NSLOT, RING = Sch::RING;
-    static_assert(TILE_CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
+    static_assert(TILE_CHUNKS % NT == 0, "tile must split evenly over the workgroup's threads");
 
     __shared__ __attribute__((aligned(1024))) T smem[6][BN * D];   // K slots 0-2, V slots 3-5
     const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) T *)smem[0];
@@ -228,16 +268,21 @@ void attn_fwd_w64_kernel(AttnParams p) {
         kp = (const T *)p.k + b_ * p.k_sb + h_ * p.k_sh;
         vp = (const T *)p.v + b_ * p.v_sb + h_ * p.v_sh;
     };
+    // Rows of the wave within the item.  With two waves per SIMD (waves w and
+    // w + 4 share a SIMD), wave w < 4 takes rows 32 w and wave w >= 4 rows
+    // 32 (11 - w), so each SIMD holds one block of the upper and one of the
+    // lower half of the tile and the SIMDs see equal causal work.
+    const int wave_row = NW == 4 ? 32 * QB * wave : 32 * (wave < 4 ? wave : 11 - wave);
     auto set_item = [&](int L) __attribute__((always_inline)) {
         map_index<CAUSAL>(p, L, bh, qt);
-        q0w = qt * kBlockM + 64 * wave;   // first row of the wave
+        q0w = qt * kBlockM + wave_row;    // first row of the wave
         nt = item_tiles(qt);
         nt2 = (nt + 1) & ~1;              // iterations run by every wave
         wave_active = q0w < S;
         // Tiles this wave computes: 0 .. ntw-1; only tile ntw-1 can hold keys
         // past a row of the wave (causal diagonal) or past S.  Rounded up to
         // even, the extra tile being fully masked.
-        ntw = !wave_active ? 0 : CAUSAL ? min(nt, (q0w + 63) / BN + 1) : nt;
+        ntw = !wave_active ? 0 : CAUSAL ? min(nt, (q0w + 32 * QB - 1) / BN + 1) : nt;
         ntw2 = (ntw + 1) & ~1;
         head_ptrs(bh, kg, vg);
     };
@@ -253,12 +298,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
 
     // Q fragments of the current item (B operand of S^T = K Q^T, AGPRs):
     // block qb, lane holds Q[q0w + 32 qb + col][16 dk + 8 hi .. +7].
-    frag qf[2][NDK];
+    frag qf[QB][NDK];
     auto load_q = [&]() __attribute__((always_inline)) {
         const int b_ = bh / p.H, h_ = bh - b_ * p.H;
         const T *qg = (const T *)p.q + b_ * p.q_sb + h_ * p.q_sh;
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             const int qrow = min(q0w + 32 * qb + col, S - 1);
             const T *src = qg + (int64_t)qrow * p.q_ss + 8 * hi;
 #pragma unroll
@@ -272,18 +317,18 @@ void attn_fwd_w64_kernel(AttnParams p) {
     // the load latency overlaps them.
     auto pin_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
             for (int dk = 0; dk < NDK; ++dk) asm volatile("" : "+a"(qf[qb][dk]));
     };
 
     // ---- DMA staging: lane `lane` of wave `wave` fills chunk slot
-    // j*256 + 64*wave + lane, i.e. LDS bytes slot_base + 4096 j + 1024 wave
+    // j*NT + 64*wave + lane, i.e. LDS bytes slot_base + 16 NT j + 1024 wave
     // + 16 lane, with the logical chunk the XOR swizzle places there.
     int koff[LOADS], voff[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-        const int sl = j * 256 + tid;
+        const int sl = j * NT + tid;
         const int row = sl / CPR;
         const int pc = sl % CPR;
         koff[j] = (int)((row * p.k_ss + 8 * (pc ^ swz_k<CPR>(row))) * (int64_t)sizeof(T));
@@ -306,14 +351,14 @@ void attn_fwd_w64_kernel(AttnParams p) {
         const T *base = nx ? kg_n : kg;
         const int tile = nx ? min(kt - nt2, nt_n - 1) : min(kt, nt - 1);
         w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, k_records, 0x00020000),
-                      koff[j] + tile * k_tile_bytes, lds_w + (unsigned)(sl * TILE_BYTES + j * 4096));
+                      koff[j] + tile * k_tile_bytes, lds_w + (unsigned)(sl * TILE_BYTES + j * 16 * NT));
     };
     auto dma_v = [&](int kt, int sl, int j) __attribute__((always_inline)) {
         const bool nx = has_next && kt >= nt2;
         const T *base = nx ? vg_n : vg;
         const int tile = nx ? min(kt - nt2, nt_n - 1) : min(kt, nt - 1);
         w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, v_records, 0x00020000),
-                      voff[j] + tile * v_tile_bytes, lds_w + (unsigned)((3 + sl) * TILE_BYTES + j * 4096));
+                      voff[j] + tile * v_tile_bytes, lds_w + (unsigned)((3 + sl) * TILE_BYTES + j * 16 * NT));
     };
     // DMA i of iteration t: K(t+3) into slot t % 3 (sl0), then V(t+2) into
     // slot (t+2) % 3 (sl2).
@@ -330,19 +375,30 @@ void attn_fwd_w64_kernel(AttnParams p) {
     };
 
     // Softmax state of the current item (reset per item).
-    f32x16_t acc[2][NDB];      // O^T accumulators, AGPRs
-    f32x16_t sc[2][2][2];      // [set][qb][kb] scores; tile t uses set t & 1
-    uint32_t pk[2][2][8];      // [qb][kb][pair] probabilities of the tile in PV
+    f32x16_t acc[QB][NDB];     // O^T accumulators, AGPRs
+    f32x16_t sc[2][QB][2];     // [set][qb][kb] scores; tile t uses set t & 1
+    uint32_t pk[QB][2][8];     // [qb][kb][pair] probabilities of the tile in PV
     float pe[2][2];            // exponentials of a pair until packed, by pair parity
-    float m_true[2], m_use[2];
-    float moff[2];             // -m_use * scale_log2 (0 while m_use is -inf)
-    float alpha[2];
-    bool rescale[2];
-    float l_a[2], l_b[2];      // two partial row sums per block
+    float m_true[QB], m_use[QB];
+    float moff[QB];            // -m_use * scale_log2 (0 while m_use is -inf)
+    float alpha[QB];
+    bool rescale[QB];
+    // Row sums: an MFMA of an all-ones A operand with the packed
+    // probabilities adds each query column's sum of the rounded P to every
+    // register of lsum (AGPRs), so O is normalised by exactly the weights the
+    // PV product used, and the sums cost no vector instructions.
+    f32x16_t lsum[QB];
+    frag ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones[i] = (T)1.0f;
+    // Opaque from here on: kept in four VGPRs instead of being rebuilt from
+    // SGPRs by VALU moves right before each MFMA that reads it (the MFMAs
+    // are inline asm, so the compiler inserts no wait states for them).
+    asm volatile("" : "+v"(ones));
     const float lazy_raw = kLazyLog2 / p.scale_log2;
     auto reset_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -351,7 +407,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
             moff[qb] = 0.f;
             alpha[qb] = 1.f;
             rescale[qb] = false;
-            l_a[qb] = l_b[qb] = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) lsum[qb][r] = 0.f;
         }
     };
 
@@ -399,7 +456,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
         if (__builtin_expect(kt >= ntw - 1, 0)) {
             const int kbase = kt * BN;
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
+            for (int qb = 0; qb < QB; ++qb) {
                 const int qi = q0w + 32 * qb + col;
                 const int lim = kt == ntw - 1 ? (CAUSAL ? min(qi, S - 1) : S - 1) : -1;
 #pragma unroll
@@ -414,27 +471,28 @@ void attn_fwd_w64_kernel(AttnParams p) {
             }
         }
     };
-    float mx[2], mh[2];
-    // Max unit k of score set SET: k < 8 partial row max (qb, kb, half);
-    // k = 8, 9 the row max of block k - 8 (both lane halves); k = 10, 11 the
-    // update of block k - 10: exact running max and the lazy rescale decision,
-    // without branches (the O rescale itself waits for the PV MFMAs in flight).
-    // Split so that no dependency chain stalls the in-order issue for long.
+    float mx[QB], mh[QB];
+    // Max unit k of score set SET: k < 4 QB partial row max (qb, kb, half);
+    // k in [4 QB, 5 QB) the row max of block k - 4 QB (both lane halves);
+    // k in [5 QB, 6 QB) the update of block k - 5 QB: exact running max and
+    // the lazy rescale decision, without branches (the O rescale itself waits
+    // for the PV MFMAs in flight).  Split so that no dependency chain stalls
+    // the in-order issue for long.
     auto max_unit = [&](auto set_c, int k) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
-        if (k < 8) {
+        if (k < 4 * QB) {
             const int qb = k >> 2, kb = (k >> 1) & 1, r0 = 8 * (k & 1);
             float m = (k & 3) == 0 ? sc[SET][qb][0][0] : mx[qb];
 #pragma unroll
             for (int r = 0; r < 8; ++r) m = fmaxf(m, sc[SET][qb][kb][r0 + r]);
             asm volatile("" : "+v"(m));
             mx[qb] = m;
-        } else if (k < 10) {
-            const int qb = k - 8;
+        } else if (k < 5 * QB) {
+            const int qb = k - 4 * QB;
             mh[qb] = half_max(mx[qb]);
             asm volatile("" : "+v"(mh[qb]));
         } else {
-            const int qb = k - 10;
+            const int qb = k - 5 * QB;
             const float m = mh[qb];
             m_true[qb] = fmaxf(m_true[qb], m);
             const bool up = __builtin_amdgcn_ballot_w64(m > m_use[qb] + lazy_raw) != 0;
@@ -446,19 +504,20 @@ void attn_fwd_w64_kernel(AttnParams p) {
             moff[qb] = up ? mo : moff[qb];
         }
     };
-    // The O^T accumulators of block qb at a drain.
+    // The O^T accumulators and row sums of block qb at a drain.
     auto fence_block = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) w64_fence_a(acc[qb][db]);
+        w64_fence_a(lsum[qb]);
     };
     auto apply_rescale = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
             if (__builtin_expect(rescale[qb], 0)) {
-                l_a[qb] *= alpha[qb];
-                l_b[qb] *= alpha[qb];
                 w64_mfma_drain();
                 fence_block(qb);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) lsum[qb][r] *= alpha[qb];
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -480,14 +539,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
             pe[i & 1][kind] = fast_exp2(__builtin_fmaf(sc[SET][qb][kb][r + kind], p.scale_log2, moff[qb]));
             asm volatile("" : "+v"(pe[i & 1][kind]));
         } else {
-            // The row sums take the probabilities as rounded for the PV
-            // product, so O is normalised by exactly the weights it was
-            // built from.
-            const uint32_t w = E::pack2(pe[i & 1][0], pe[i & 1][1]);
-            pk[qb][kb][r >> 1] = w;
-            l_a[qb] = E::add_lo(w, l_a[qb]);
-            l_b[qb] = E::add_hi(w, l_b[qb]);
-            asm volatile("" : "+v"(pk[qb][kb][r >> 1]), "+v"(l_a[qb]), "+v"(l_b[qb]));
+            pk[qb][kb][r >> 1] = E::pack2(pe[i & 1][0], pe[i & 1][1]);
+            asm volatile("" : "+v"(pk[qb][kb][r >> 1]));
         }
     };
 
@@ -504,21 +557,26 @@ void attn_fwd_w64_kernel(AttnParams p) {
         const T *Vs = smem[3 + sl0];
         w64_static_for<0, NSLOT>([&](auto s_c) __attribute__((always_inline)) {
             constexpr int s = decltype(s_c)::value;
-            constexpr int g = s >> 1, qb = s & 1;
+            constexpr int kd = Sch::kind(s), qb = Sch::qb_of(s);
+            constexpr int g = kd == Sch::SUM ? 0 : Sch::frag_of(s);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (g < NKF) {
+            if constexpr (kd == Sch::QK) {
                 constexpr int dk = g >> 1, kb = g & 1;
                 if constexpr (dk == 0) M::qk0(sc[SET ^ 1][qb][kb], ring[g % RING], qf[qb][0]);
                 else M::qk(sc[SET ^ 1][qb][kb], ring[g % RING], qf[qb][dk]);
-            } else {
+            } else if constexpr (kd == Sch::PV) {
                 constexpr int f = g - NKF;
                 constexpr int kb = f / (2 * NDB), c = (f / NDB) % 2, db = f % NDB;
                 u32x4_t bw = {pk[qb][kb][4 * c], pk[qb][kb][4 * c + 1], pk[qb][kb][4 * c + 2], pk[qb][kb][4 * c + 3]};
                 M::pv(acc[qb][db], ring[g % RING], __builtin_bit_cast(frag, bw));
+            } else {
+                constexpr int grp = Sch::group_of(s), kb = grp >> 1, c = grp & 1;
+                u32x4_t bw = {pk[qb][kb][4 * c], pk[qb][kb][4 * c + 1], pk[qb][kb][4 * c + 2], pk[qb][kb][4 * c + 3]};
+                M::pv(lsum[qb], ones, __builtin_bit_cast(frag, bw));
             }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (s == Sch::BARS) sync_tiles();
-            if constexpr (qb == 1) {   // fragment g is done: refill its ring entry
+            if constexpr (kd != Sch::SUM && qb == QB - 1) {   // fragment g is done: refill its ring entry
                 constexpr int gn = g + RING;
                 if constexpr (gn < NKF) ring[g % RING] = kfrag(kcur, gn);
                 else if constexpr (gn < NF) ring[g % RING] = vfrag(Vs, gn - NKF);
@@ -531,7 +589,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
             if constexpr (s == Sch::MS0) {
                 w64_mfma_drain();   // the QK MFMAs of tile t+1 have written the scores
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb)
+                for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb) w64_fence_v(sc[SET ^ 1][qb][kb]);
                 sm_mask(t + 1, NSET{});
@@ -560,8 +618,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
         const int b_ = bh_e / p.H, h_ = bh_e - b_ * p.H;
         T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const float l_sum = half_sum(l_a[qb] + l_b[qb]);   // relative to m_use
+        for (int qb = 0; qb < QB; ++qb) {
+            const float l_sum = lsum[qb][0];   // relative to m_use, both lane halves
             const int qi = q0w_e + 32 * qb + col;
             const bool ok = active_e && qi < S;
             const float inv = 1.0f / l_sum;                    // not stored where !ok
@@ -631,14 +689,14 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 const frag a = kfrag(k0, f);
                 const int dk = f >> 1, kb = f & 1;
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) {
+                for (int qb = 0; qb < QB; ++qb) {
                     if (dk == 0) M::qk0(sc[0][qb][kb], a, qf[qb][0]);
                     else M::qk(sc[0][qb][kb], a, qf[qb][dk]);
                 }
             }
             w64_mfma_drain();
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
+            for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) w64_fence_v(sc[0][qb][kb]);
             sm_mask(0, S0{});
@@ -674,8 +732,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
             sc3 = tmp;
         }
         w64_mfma_drain();   // the last PV MFMAs have written O
-        fence_block(0);
-        fence_block(1);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) fence_block(qb);
 
         // Next item first (its Q loads overlap this item's epilogue), then
         // this item's outputs.
