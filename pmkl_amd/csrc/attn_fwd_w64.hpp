@@ -67,7 +67,17 @@ __device__ __forceinline__ void w64_lds_dma16(__amdgpu_buffer_rsrc_t r, int off,
 //   qk0   d (VGPRs)  = a * b (b in AGPRs)
 //   qk    d (VGPRs) += a * b (b in AGPRs)
 template <typename T> struct W64Mma;
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <> struct W64Mma<__bf16> {
+    typedef bf16x4_t half_frag;
+    // c (AGPRs) += a * b over 16 blocks of 4x4x4: lane 4 i + j of block i
+    // holds column j of b, so with a = 1 every register of a lane receives the
+    // sum of the lane's own four values of b.
+    static __device__ __forceinline__ void sum4(f32x4_t &c, bf16x4_t a, bf16x4_t b) {
+        asm volatile("v_mfma_f32_4x4x4_16b_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
     static __device__ __forceinline__ void pv(f32x16_t &c, bf16x8_t a, bf16x8_t b) {
         asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
     }
@@ -79,6 +89,10 @@ template <> struct W64Mma<__bf16> {
     }
 };
 template <> struct W64Mma<_Float16> {
+    typedef f16x4_t half_frag;
+    static __device__ __forceinline__ void sum4(f32x4_t &c, f16x4_t a, f16x4_t b) {
+        asm volatile("v_mfma_f32_4x4x4_16b_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    }
     static __device__ __forceinline__ void pv(f32x16_t &c, f16x8_t a, f16x8_t b) {
         asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
     }
@@ -98,6 +112,7 @@ template <> struct W64Mma<_Float16> {
 // above the drain and no write below it.
 __device__ __forceinline__ void w64_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 __device__ __forceinline__ void w64_fence_a(f32x16_t &x) { asm volatile("" : "+a"(x)); }
+__device__ __forceinline__ void w64_fence_a(f32x4_t &x) { asm volatile("" : "+a"(x)); }
 __device__ __forceinline__ void w64_fence_v(f32x16_t &x) { asm volatile("" : "+v"(x)); }
 
 // s = (R <= d) ? s : -inf, through VCC: left to itself the compiler computes
@@ -121,8 +136,9 @@ __device__ __forceinline__ void w64_static_for(F &&f) {
 // blocks per wave), one MFMA per slot:
 //   slots 0 .. QKS-1      QK of tile t+1: fragment s / QB, block s % QB
 //   then 4 groups (kb, c) of GS slots: the NDB QB PV MFMAs of the group
-//   (fragment, block), then QB row-sum MFMAs (block), which add the group's
-//   packed probabilities into the row sums (all-ones A operand).
+//   (fragment, block), then 2 QB row-sum MFMAs (4x4x4, all-ones A operand),
+//   each adding half of a block's packed probabilities of the group into the
+//   row sums.
 template <int D, int QB> struct W64Sched {
     static constexpr int NDB = D / 32;            // 32-wide blocks of head_dim
     static constexpr int NDK = D / 16;            // 16-deep MFMA steps over head_dim
@@ -130,7 +146,7 @@ template <int D, int QB> struct W64Sched {
     static constexpr int NVF = 4 * NDB;           // V^T fragments per tile: (kb, c, db)
     static constexpr int NF = NKF + NVF;          // fragments per iteration
     static constexpr int QKS = QB * NKF;          // first PV slot
-    static constexpr int GS = QB * (NDB + 1);     // slots per PV group
+    static constexpr int GS = QB * (NDB + 2);     // slots per PV group
     static constexpr int NSLOT = QKS + 4 * GS;    // MFMAs per iteration
     static constexpr int RING = 4;                // fragments read ahead
     enum { QK = 0, PV = 1, SUM = 2 };
@@ -140,8 +156,9 @@ template <int D, int QB> struct W64Sched {
         return s < QKS ? s / QB : NKF + ((s - QKS) / GS) * NDB + ((s - QKS) % GS) / QB;
     }
     static constexpr int qb_of(int s) {
-        return s < QKS ? s % QB : (s - QKS) % GS < NDB * QB ? ((s - QKS) % GS) % QB : (s - QKS) % GS - NDB * QB;
+        return s < QKS ? s % QB : (s - QKS) % GS < NDB * QB ? ((s - QKS) % GS) % QB : ((s - QKS) % GS - NDB * QB) % QB;
     }
+    static constexpr int sum_half(int s) { return ((s - QKS) % GS - NDB * QB) / QB; }   // SUM slots
     static constexpr int group_of(int s) { return (s - QKS) / GS; }
     // slot of fragment g's last-block MFMA, after which its ring entry is refilled
     static constexpr int last_slot(int g) {
@@ -166,7 +183,7 @@ template <int D, int QB> struct W64Sched {
     // (pack), in the stream A0 B0 A1 B1 C0 A2 B2 C1 ... A(NP-1) B(NP-1)
     // C(NP-2) C(NP-1), spread evenly over slots 0 .. ES-1.
     static constexpr int NU = 3 * NP;
-    static constexpr int ES = QKS + 3 * GS - 1;
+    static constexpr int ES = QKS + 3 * GS - 2 * QB - 1;
     static constexpr int unit_slot(int n) { return n * ES / NU; }
     static constexpr int unit_first(int s) { return (s * NU + ES - 1) / ES; }   // first unit of slot s
     static constexpr int unit_kind(int n) { return n < 2 ? n : n == NU - 1 ? 2 : (n - 2) % 3; }
@@ -189,8 +206,10 @@ template <int D, int QB> struct W64Sched {
             if (unit_slot(n) < 0 || unit_slot(n) >= ES || unit_first(unit_slot(n)) > n ||
                 unit_first(unit_slot(n) + 1) <= n)
                 return false;
+        // P packed a full slot before the row-sum slots that precede its PV
+        // group (those are short 4x4x4 MFMAs).
         for (int i = 0; i < NP; ++i)
-            if (unit_slot(c_unit(i)) > pair_need(i) - 2) return false;   // P ready a slot early
+            if (unit_slot(c_unit(i)) > pair_need(i) - 2 * QB - 2) return false;
         // The block updates change the exponent offsets: after every exponential.
         if (max_slot(5 * QB) < ES) return false;
         if (max_slot(NMU - 1) != NSLOT - 1) return false;
@@ -255,7 +274,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     };
 
     // Current item.
-    int bh = 0, qt = 0, q0w = 0, nt = 1, nt2 = 2, ntw = 0, ntw2 = 0;
+    int bh = 0, qt = 0, q0w = 0, nt = 1, nt2 = 2, ntw = 0;
     bool wave_active = false;
     const T *kg = nullptr, *vg = nullptr;
     // Next item: its first tiles are loaded during the current item's last
@@ -280,10 +299,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
         nt2 = (nt + 1) & ~1;              // iterations run by every wave
         wave_active = q0w < S;
         // Tiles this wave computes: 0 .. ntw-1; only tile ntw-1 can hold keys
-        // past a row of the wave (causal diagonal) or past S.  Rounded up to
-        // even, the extra tile being fully masked.
+        // past a row of the wave (causal diagonal) or past S.
         ntw = !wave_active ? 0 : CAUSAL ? min(nt, (q0w + 32 * QB - 1) / BN + 1) : nt;
-        ntw2 = (ntw + 1) & ~1;
         head_ptrs(bh, kg, vg);
     };
     auto set_next = [&](int L) __attribute__((always_inline)) {
@@ -383,14 +400,16 @@ void attn_fwd_w64_kernel(AttnParams p) {
     float moff[QB];            // -m_use * scale_log2 (0 while m_use is -inf)
     float alpha[QB];
     bool rescale[QB];
-    // Row sums: an MFMA of an all-ones A operand with the packed
-    // probabilities adds each query column's sum of the rounded P to every
-    // register of lsum (AGPRs), so O is normalised by exactly the weights the
-    // PV product used, and the sums cost no vector instructions.
-    f32x16_t lsum[QB];
-    frag ones;
+    // Row sums: 4x4x4 MFMAs of an all-ones A operand with the packed
+    // probabilities add each lane's own rounded P to every register of its
+    // lsum (AGPRs; the two lane halves are combined at the end), so O is
+    // normalised by exactly the weights the PV product used, and the sums cost
+    // no vector instructions.
+    using half_frag = typename M::half_frag;
+    f32x4_t lsum[QB];
+    half_frag ones;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ones[i] = (T)1.0f;
+    for (int i = 0; i < 4; ++i) ones[i] = (T)1.0f;
     // Opaque from here on: kept in four VGPRs instead of being rebuilt from
     // SGPRs by VALU moves right before each MFMA that reads it (the MFMAs
     // are inline asm, so the compiler inserts no wait states for them).
@@ -408,7 +427,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
             alpha[qb] = 1.f;
             rescale[qb] = false;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) lsum[qb][r] = 0.f;
+            for (int r = 0; r < 4; ++r) lsum[qb][r] = 0.f;
         }
     };
 
@@ -517,7 +536,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 w64_mfma_drain();
                 fence_block(qb);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) lsum[qb][r] *= alpha[qb];
+                for (int r = 0; r < 4; ++r) lsum[qb][r] *= alpha[qb];
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -570,9 +589,9 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 u32x4_t bw = {pk[qb][kb][4 * c], pk[qb][kb][4 * c + 1], pk[qb][kb][4 * c + 2], pk[qb][kb][4 * c + 3]};
                 M::pv(acc[qb][db], ring[g % RING], __builtin_bit_cast(frag, bw));
             } else {
-                constexpr int grp = Sch::group_of(s), kb = grp >> 1, c = grp & 1;
-                u32x4_t bw = {pk[qb][kb][4 * c], pk[qb][kb][4 * c + 1], pk[qb][kb][4 * c + 2], pk[qb][kb][4 * c + 3]};
-                M::pv(lsum[qb], ones, __builtin_bit_cast(frag, bw));
+                constexpr int grp = Sch::group_of(s), kb = grp >> 1, c = grp & 1, h = Sch::sum_half(s);
+                u32x2_t bw = {pk[qb][kb][4 * c + 2 * h], pk[qb][kb][4 * c + 2 * h + 1]};
+                M::sum4(lsum[qb], ones, __builtin_bit_cast(half_frag, bw));
             }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (s == Sch::BARS) sync_tiles();
@@ -619,7 +638,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
         T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            const float l_sum = lsum[qb][0];   // relative to m_use, both lane halves
+            const float l_sum = half_sum(lsum[qb][0]);   // relative to m_use
             const int qi = q0w_e + 32 * qb + col;
             const bool ok = active_e && qi < S;
             const float inv = 1.0f / l_sum;                    // not stored where !ok
@@ -711,15 +730,25 @@ void attn_fwd_w64_kernel(AttnParams p) {
             for (int f = 0; f < RING; ++f) ring[f] = kfrag(k1, f);
         }
 
-        // ---- tiles the wave computes, two per iteration (score sets 0, 1) ----
+        // ---- tiles the wave computes, two per iteration (score sets 0, 1),
+        // an odd last one alone ----
         int t = 0;
-        for (; t < ntw2; t += 2) {
+        while (t < ntw) {
             iteration(t, S0{}, sa, sb, sc3);
+            if (t + 1 == ntw) {
+                const int tmp = sa;
+                sa = sb;
+                sb = sc3;
+                sc3 = tmp;
+                ++t;
+                break;
+            }
             iteration(t + 1, S1{}, sb, sc3, sa);
             const int tmp = sa;
             sa = sc3;
             sc3 = sb;
             sb = tmp;
+            t += 2;
         }
         // ---- remaining tiles of the item: DMAs and barriers only ----
         for (; t < nt2; ++t) {
