@@ -181,16 +181,25 @@ template <int D, int QB> struct W64Sched {
 
     // Exponential units, three per pair: A (first exp), B (second), C
     // (pack), in the stream A0 B0 A1 B1 C0 A2 B2 C1 ... A(NP-1) B(NP-1)
-    // C(NP-2) C(NP-1), spread evenly over slots 0 .. ES-1.
+    // C(NP-2) C(NP-1), spread evenly over slots 0 .. ES-1. ES is the widest
+    // spread (at most QKS + 3 GS - 2 QB - 1) that packs every pair a full slot
+    // before the row-sum slots preceding its PV group (those are short 4x4x4
+    // MFMAs); at head_dim 32 the groups are short and the spread narrows.
     static constexpr int NU = 3 * NP;
-    static constexpr int ES = QKS + 3 * GS - 2 * QB - 1;
+    static constexpr int c_unit(int i) { return i == NP - 1 ? NU - 1 : 3 * i + 4; }
+    static constexpr bool packs_in_time(int es) {
+        for (int i = 0; i < NP; ++i)
+            if (c_unit(i) * es / NU > pair_need(i) - 2 * QB - 2) return false;
+        return true;
+    }
+    static constexpr int widest_spread(int es) { return es <= 1 || packs_in_time(es) ? es : widest_spread(es - 1); }
+    static constexpr int ES = widest_spread(QKS + 3 * GS - 2 * QB - 1);
     static constexpr int unit_slot(int n) { return n * ES / NU; }
     static constexpr int unit_first(int s) { return (s * NU + ES - 1) / ES; }   // first unit of slot s
     static constexpr int unit_kind(int n) { return n < 2 ? n : n == NU - 1 ? 2 : (n - 2) % 3; }
     static constexpr int unit_pair(int n) {
         return n < 2 ? 0 : n == NU - 1 ? NP - 1 : (n - 2) % 3 == 2 ? (n - 2) / 3 : (n - 2) / 3 + 1;
     }
-    static constexpr int c_unit(int i) { return i == NP - 1 ? NU - 1 : 3 * i + 4; }
 
     // Maxima of tile t+1: drain and mask at slot MS0, then 4 QB partial maxima
     // (qb, kb, half), the QB block maxima and the QB block updates.
@@ -206,10 +215,7 @@ template <int D, int QB> struct W64Sched {
             if (unit_slot(n) < 0 || unit_slot(n) >= ES || unit_first(unit_slot(n)) > n ||
                 unit_first(unit_slot(n) + 1) <= n)
                 return false;
-        // P packed a full slot before the row-sum slots that precede its PV
-        // group (those are short 4x4x4 MFMAs).
-        for (int i = 0; i < NP; ++i)
-            if (unit_slot(c_unit(i)) > pair_need(i) - 2 * QB - 2) return false;
+        if (!packs_in_time(ES)) return false;
         // The block updates change the exponent offsets: after every exponential.
         if (max_slot(5 * QB) < ES) return false;
         if (max_slot(NMU - 1) != NSLOT - 1) return false;
@@ -404,9 +410,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
     // probabilities add each lane's own rounded P to every register of its
     // lsum (AGPRs; the two lane halves are combined at the end), so O is
     // normalised by exactly the weights the PV product used, and the sums cost
-    // no vector instructions.
+    // no vector instructions.  One accumulator per (block, half of a group's
+    // P): the row-sum MFMAs of a group run back to back, and a 4x4x4 result
+    // is not ready for the SrcC read of the very next MFMA; on one
+    // accumulator they are a whole group apart.
     using half_frag = typename M::half_frag;
-    f32x4_t lsum[QB];
+    f32x4_t lsum[QB][2];
     half_frag ones;
 #pragma unroll
     for (int i = 0; i < 4; ++i) ones[i] = (T)1.0f;
@@ -427,7 +436,9 @@ void attn_fwd_w64_kernel(AttnParams p) {
             alpha[qb] = 1.f;
             rescale[qb] = false;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) lsum[qb][r] = 0.f;
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) lsum[qb][h][r] = 0.f;
         }
     };
 
@@ -527,7 +538,8 @@ void attn_fwd_w64_kernel(AttnParams p) {
     auto fence_block = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) w64_fence_a(acc[qb][db]);
-        w64_fence_a(lsum[qb]);
+        w64_fence_a(lsum[qb][0]);
+        w64_fence_a(lsum[qb][1]);
     };
     auto apply_rescale = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -536,7 +548,10 @@ void attn_fwd_w64_kernel(AttnParams p) {
                 w64_mfma_drain();
                 fence_block(qb);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) lsum[qb][r] *= alpha[qb];
+                for (int r = 0; r < 4; ++r) {
+                    lsum[qb][0][r] *= alpha[qb];
+                    lsum[qb][1][r] *= alpha[qb];
+                }
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -591,7 +606,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
             } else {
                 constexpr int grp = Sch::group_of(s), kb = grp >> 1, c = grp & 1, h = Sch::sum_half(s);
                 u32x2_t bw = {pk[qb][kb][4 * c + 2 * h], pk[qb][kb][4 * c + 2 * h + 1]};
-                M::sum4(lsum[qb], ones, __builtin_bit_cast(half_frag, bw));
+                M::sum4(lsum[qb][h], ones, __builtin_bit_cast(half_frag, bw));
             }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (s == Sch::BARS) sync_tiles();
@@ -638,7 +653,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
         T *og = (T *)p.o + b_ * p.o_sb + h_ * p.o_sh;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            const float l_sum = half_sum(lsum[qb][0]);   // relative to m_use
+            const float l_sum = half_sum(lsum[qb][0][0] + lsum[qb][1][0]);   // relative to m_use
             const int qi = q0w_e + 32 * qb + col;
             const bool ok = active_e && qi < S;
             const float inv = 1.0f / l_sum;                    // not stored where !ok
