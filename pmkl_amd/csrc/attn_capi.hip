@@ -66,7 +66,9 @@ KernelChoice pick16w(bool causal) {
             NW * 64, NW * 32};
 }
 // 64-row kernel choice: PMKL_ATTN_W64=0 never, =1 wherever it applies,
-// unset: for head_dim 128 (at 32 and 64 the 4- or 8-wave kernel is faster).
+// unset: for head_dim 128, and for causal head_dim 64 from S = 512 on (in its
+// two-wave layout, measured 5-35% faster there; non-causal and at S <= 384
+// the 8-wave kernel is faster, as at head_dim 32).
 int w64_mode() {
     static const int v = [] {
         const char *e = getenv("PMKL_ATTN_W64");
@@ -96,9 +98,10 @@ int cu_count() {
     return n;
 }
 
-// Layout of the 64-row kernel at head_dim 128: by default two waves of 32
-// rows per SIMD (8 waves per workgroup, measured 4-6% faster at C3 and equal
-// at C4); PMKL_ATTN_W32=0 keeps one wave of 64 rows per SIMD.
+// Layout of the 64-row kernel at head_dim 64 and 128: by default two waves
+// of 32 rows per SIMD (8 waves per workgroup, measured 4-6% faster at C3,
+// equal at C4, 15% faster at C2); PMKL_ATTN_W32=0 keeps one wave of 64 rows
+// per SIMD.
 int w32_mode() {
     static const int v = [] {
         const char *e = getenv("PMKL_ATTN_W32");
@@ -107,11 +110,15 @@ int w32_mode() {
     return v;
 }
 
-template <typename T>
+template <typename T, int D>
 KernelChoice pick_w32(bool causal) {
-    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 128, true, 1, 8>
-                   : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 128, false, 1, 8>,
+    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, true, 1, 8>
+                   : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false, 1, 8>,
             512, 256};
+}
+template <typename T>
+KernelChoice pick_w32(int64_t D, bool causal) {
+    return D == 64 ? pick_w32<T, 64>(causal) : pick_w32<T, 128>(causal);
 }
 
 template <typename T, int D>
@@ -402,12 +409,13 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
         return st[2] >= 0 && ((S - 1) * st[2] + D) * (int64_t)es < (1LL << 31);
     };
     const int mode = w64_mode();
-    const bool w64 = mode != 0 && (mode == 1 || D >= 128) && a->dtype != PMKL_DTYPE_F32 && S > 128 &&
-                     head_span_ok(ks) && head_span_ok(vs);
-    const bool w32 = w64 && D == 128 && w32_mode() == 1;
+    const bool causal = a->is_causal != 0;
+    const bool w64 = mode != 0 && (mode == 1 || D >= 128 || (D == 64 && causal && S >= 512)) &&
+                     a->dtype != PMKL_DTYPE_F32 && S > 128 && head_span_ok(ks) && head_span_ok(vs);
+    const bool w32 = w64 && (D == 64 || D == 128) && w32_mode() == 1;
     const bool bf = a->dtype == PMKL_DTYPE_BF16;
-    const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(a->is_causal != 0) : pick_w32<_Float16>(a->is_causal != 0))
-                                : select_kernel(a->dtype, D, a->is_causal != 0, w64, waves16(D, S, a->is_causal != 0));
+    const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(D, causal) : pick_w32<_Float16>(D, causal))
+                                : select_kernel(a->dtype, D, causal, w64, waves16(D, S, causal));
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
     const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;

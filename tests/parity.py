@@ -62,28 +62,45 @@ def check_outputs(q, k, v, o, m, l, dtype: str, causal: bool = True, rows=None, 
     err_m = np.abs(mn - m_ref)
     err_l = np.abs(ln - l_ref)
     worst = float(np.max(diff / bound)) if on.size else 0.0
+    plain = half_ulp < tol
+    err_plain = float(diff[plain].max()) if plain.any() else 0.0
+    if dtype == "fp32":
+        ulps_m = ulps_l = None
+    else:
+        um = oracle.ulp(m_ref, MANT_BITS[dtype])
+        ul = oracle.ulp(l_ref, MANT_BITS[dtype])
+        ulps_m = float((err_m / um).max()) if err_m.size else 0.0
+        ulps_l = float((err_l / ul).max()) if err_l.size else 0.0
+    report = {"err_o": err_o, "err_o_where_representable": err_plain, "floor_o": floor,
+              "worst_over_bound": worst,
+              "err_m": float(err_m.max()) if err_m.size else 0.0,
+              "err_l": float(err_l.max()) if err_l.size else 0.0,
+              "ulps_m": ulps_m, "ulps_l": ulps_l}
+    _log(label, dtype, (B, H, S, D), causal, rows, report)
     assert worst <= 1.0, (f"{label}: O beyond bound: max|dO| {err_o:.3g} (tol {tol}, floor {floor:.3g}, "
                           f"worst error/bound {worst:.3f})")
     if dtype == "fp32":
         assert np.all(err_m <= 1e-5 + 1e-5 * np.abs(m_ref)), f"{label}: m beyond all_close, max {err_m.max():.3g}"
         assert np.all(err_l <= 1e-5 + 1e-5 * np.abs(l_ref)), f"{label}: l beyond all_close, max {err_l.max():.3g}"
     else:
-        um = oracle.ulp(m_ref, MANT_BITS[dtype])
-        ul = oracle.ulp(l_ref, MANT_BITS[dtype])
-        assert np.all(err_m <= um), f"{label}: m beyond 1 ulp ({(err_m / um).max():.2f} ulp)"
-        assert np.all(err_l <= ul), f"{label}: l beyond 1 ulp ({(err_l / ul).max():.2f} ulp)"
-    plain = half_ulp < tol
-    err_plain = float(diff[plain].max()) if plain.any() else 0.0
-    if dtype == "fp32":
-        ulps_m = ulps_l = None
-    else:
-        ulps_m = float((err_m / oracle.ulp(m_ref, MANT_BITS[dtype])).max()) if err_m.size else 0.0
-        ulps_l = float((err_l / oracle.ulp(l_ref, MANT_BITS[dtype])).max()) if err_l.size else 0.0
-    return {"err_o": err_o, "err_o_where_representable": err_plain, "floor_o": floor,
-            "worst_over_bound": worst,
-            "err_m": float(err_m.max()) if err_m.size else 0.0,
-            "err_l": float(err_l.max()) if err_l.size else 0.0,
-            "ulps_m": ulps_m, "ulps_l": ulps_l}
+        assert np.all(err_m <= um), f"{label}: m beyond 1 ulp ({ulps_m:.2f} ulp)"
+        assert np.all(err_l <= ul), f"{label}: l beyond 1 ulp ({ulps_l:.2f} ulp)"
+    return report
+
+
+def _log(label, dtype, shape, causal, rows, report):
+    """Append one JSON line per check to the file PMKL_PARITY_LOG names (if
+    set): the per-configuration error table is built from these records."""
+    import json
+    import os
+
+    path = os.environ.get("PMKL_PARITY_LOG")
+    if not path:
+        return
+    rec = {"label": label, "dtype": dtype, "shape": list(shape), "causal": bool(causal),
+           "rows": None if rows is None else len(rows), **report}
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
 
 
 def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
