@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define PMKL_ABI_VERSION 3
+#define PMKL_ABI_VERSION 4
 
 /* Element types.  The reference dispatches on float, double, half and
  * bfloat16 (fused_self_attention.cpp:152-156); the device path implements
@@ -101,9 +101,12 @@ int pmkl_causal_attention_forward(int32_t dtype, void *out, const void *q, const
 /* 1 if a kernel is compiled for (dtype, head_dim), else 0. */
 int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim);
 
-/* Arguments of pmkl_attn_bwd.  All tensors contiguous [B, H, S, D] (m, l:
- * [B, H, S]), as the reference operator requires (fused_self_attention.cpp:
- * 181-182 checks q, k, v contiguous and makes dout contiguous).
+/* Arguments of pmkl_attn_bwd.  Tensors [B, H, S, D] with head_dim contiguous
+ * and any batch / head / seq element strides (all three zero: contiguous), as
+ * for pmkl_attn_fwd; m, l contiguous [B, H, S].  The reference operator takes
+ * contiguous q, k, v only and copies dout to contiguous
+ * (fused_self_attention.cpp:179-182, :201); strided views (BSHD, a packed
+ * QKV) need no copies here.
  * Gradients of O only, as the reference: with the forward's m and l,
  *   P_ij  = exp(s_ij - m_i) / l_i,   dP_ij = <dout_i, v_j>,
  *   dS_ij = P_ij (dP_ij - sum_j' P_ij' dP_ij'),
@@ -134,6 +137,17 @@ typedef struct pmkl_attn_bwd_args {
     int64_t head_dim;    /* 32, 64 or 128                                        */
     float scale;         /* 0 -> 1.0f / sqrtf((float)head_dim)                   */
     int32_t is_causal;
+    /* batch, head, seq strides (elements) of each [B, H, S, D] tensor; all
+       three zero: contiguous.  Multiples of 16 bytes, seq stride >= head_dim
+       (ABI version 4). */
+    int64_t dout_strides[3];
+    int64_t q_strides[3];
+    int64_t k_strides[3];
+    int64_t v_strides[3];
+    int64_t o_strides[3];
+    int64_t dq_strides[3];
+    int64_t dk_strides[3];
+    int64_t dv_strides[3];
 } pmkl_attn_bwd_args;
 
 /* Bytes of workspace pmkl_attn_bwd needs for this shape. */
@@ -163,7 +177,7 @@ int pmkl_attn_bwd_supported(int32_t dtype, int64_t head_dim);
  * call on one GPU shares that array: calls that overlap on one GPU (other
  * streams, other threads) race and must be serialised by the caller.  The
  * first call on a device looks up the array's device address (no allocation).
- * ABI version 3. */
+ * ABI version 3 (strided tensors: 4). */
 int pmkl_attn_bwd_noalloc(const pmkl_attn_bwd_args *args, void *stream);
 
 /* Thread-local text of the last error ("" if none), with the file:line of the

@@ -94,8 +94,8 @@ def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dty
     a = capi.make_args(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), out_m.data_ptr(),
                        out_l.data_ptr(), dtype=dt, ml_dtype=torch_dtype_to_pmkl(mdt), batch=B, heads=H,
                        seq_len=S, head_dim=D, is_causal=is_causal, scale=0.0 if scale is None else float(scale),
-                       q_strides=q.stride()[:3], k_strides=k.stride()[:3], v_strides=v.stride()[:3],
-                       o_strides=out.stride()[:3])
+                       q_strides=_abi_strides(q), k_strides=_abi_strides(k), v_strides=_abi_strides(v),
+                       o_strides=_abi_strides(out))
     if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1 or out.stride(3) != 1:
         raise ValueError("head_dim must be contiguous")
     rc = capi.attn_fwd_raw(a, stream)
@@ -104,27 +104,48 @@ def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dty
     return out, out_m, out_l
 
 
+def _abi_strides(t):
+    """Batch / head / seq element strides of a [B, H, S, D] tensor for the C
+    ABI.  A size-1 dimension's stride is never multiplied by a nonzero index
+    (torch leaves arbitrary values there after views), so it is passed as a
+    value the ABI accepts: 0 for batch / head, D for seq."""
+    return tuple(t.stride(i) if t.shape[i] != 1 else (t.shape[3] if i == 2 else 0) for i in range(3))
+
+
+def kernel_view(t):
+    """t itself if the kernels can address it in place (head_dim contiguous,
+    base and batch / head / seq strides multiples of 16 bytes, rows not
+    overlapping), else a contiguous copy."""
+    es = t.element_size()
+    vec = 16 // es
+    st = _abi_strides(t)
+    ok = (t.stride(3) == 1 or t.shape[3] == 1) and all(x % vec == 0 and x >= 0 for x in st) and \
+        (t.shape[2] == 1 or st[2] >= t.shape[3]) and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
+
+
 def attn_bwd(dout, q, k, v, out_m, out_l, is_causal: bool = True, scale: float | None = None, out=None,
              stream=None):
     """Backward of the attention output on ROCm tensors through pmkl_attn_bwd.
 
-    dout, q, k, v: contiguous [B, H, S, D] (fp16 / bf16); out_m, out_l: the
-    forward's [B, H, S] outputs (in q's dtype or float32).  `out` (the
-    forward's O) is optional: with it the row terms come from <dout, O>.
-    Returns (dq, dk, dv).  Runs on `stream` or torch's current stream; the
-    workspace is allocated through torch's caching allocator.
+    dout, q, k, v: [B, H, S, D] (fp32 / fp16 / bf16) with head_dim contiguous
+    and any batch / head / seq strides (multiples of 16 bytes; passed to the
+    kernels, no copies); out_m, out_l: the forward's contiguous [B, H, S]
+    outputs (in q's dtype or float32).  `out` (the forward's O, strided like
+    the inputs may be) is optional: with it the row terms come from
+    <dout, O>.  Returns contiguous (dq, dk, dv).  Runs on `stream` or torch's
+    current stream; the workspace is allocated through torch's caching
+    allocator.
     """
     import torch
 
-    for name, t in (("dout", dout), ("q", q), ("k", k), ("v", v)):
+    for name, t in (("dout", dout), ("q", q), ("k", k), ("v", v)) + ((("out", out),) if out is not None else ()):
         if not t.is_cuda:
             raise ValueError(f"attn_bwd takes ROCm device tensors ({name} is not)")
         if t.dim() != 4 or t.shape != q.shape:
-            raise ValueError("dout, q, k, v must share a 4-D shape [B, H, S, D]")
-        if not t.is_contiguous():
-            raise ValueError(f"{name} must be contiguous")
-    if out is not None and (out.shape != q.shape or not out.is_contiguous()):
-        raise ValueError("out must be a contiguous [B, H, S, D] tensor")
+            raise ValueError("dout, q, k, v (and out) must share a 4-D shape [B, H, S, D]")
+        if t.stride(3) != 1 and t.shape[3] != 1:
+            raise ValueError(f"{name}: head_dim must be contiguous")
     if out_m.shape != q.shape[:3] or out_l.shape != q.shape[:3] or not (out_m.is_contiguous() and out_l.is_contiguous()):
         raise ValueError("out_m / out_l must be contiguous [B, H, S] tensors")
     B, H, S, D = q.shape
@@ -133,16 +154,20 @@ def attn_bwd(dout, q, k, v, out_m, out_l, is_causal: bool = True, scale: float |
     lib = capi.load()
     ws_bytes = int(lib.pmkl_attn_bwd_workspace_size(B, H, S))
     ws = torch.empty((max(ws_bytes, 16) + 3) // 4, dtype=torch.float32, device=q.device)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
+    dq = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    dk = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    dv = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
+    strides = {"dout": _abi_strides(dout), "q": _abi_strides(q), "k": _abi_strides(k), "v": _abi_strides(v)}
+    if out is not None:
+        strides["o"] = _abi_strides(out)
     a = capi.make_bwd_args(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                            0 if out is None else out.data_ptr(), out_m.data_ptr(),
                            out_l.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                            ws.data_ptr(), ws.numel() * 4, dtype=dt, ml_dtype=mdt, batch=B, heads=H, seq_len=S,
-                           head_dim=D, is_causal=is_causal, scale=0.0 if scale is None else float(scale))
+                           head_dim=D, is_causal=is_causal, scale=0.0 if scale is None else float(scale),
+                           strides=strides)
     rc = capi.attn_bwd_raw(a, stream)
     if rc != capi.PMKL_OK:
         raise capi.PmklError(rc, capi.last_error())

@@ -89,7 +89,18 @@ class AttnBwdArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int64),
         ("scale", ctypes.c_float),
         ("is_causal", ctypes.c_int32),
+        ("dout_strides", ctypes.c_int64 * 3),
+        ("q_strides", ctypes.c_int64 * 3),
+        ("k_strides", ctypes.c_int64 * 3),
+        ("v_strides", ctypes.c_int64 * 3),
+        ("o_strides", ctypes.c_int64 * 3),
+        ("dq_strides", ctypes.c_int64 * 3),
+        ("dk_strides", ctypes.c_int64 * 3),
+        ("dv_strides", ctypes.c_int64 * 3),
     ]
+
+
+BWD_STRIDE_FIELDS = ("dout", "q", "k", "v", "o", "dq", "dk", "dv")
 
 
 class SoftmaxArgs(ctypes.Structure):
@@ -201,9 +212,15 @@ def attn_bwd_noalloc_raw(args: AttnBwdArgs, stream: int | None = None) -> int:
 
 def make_bwd_args(dout, q, k, v, o, m, l, dq, dk, dv, workspace, workspace_bytes, *, dtype: int,
                   ml_dtype: int | None = None, batch: int, heads: int, seq_len: int, head_dim: int,
-                  is_causal: bool = True, scale: float = 0.0) -> AttnBwdArgs:
-    """Build an AttnBwdArgs from raw integer pointers (o may be 0)."""
+                  is_causal: bool = True, scale: float = 0.0, strides: dict | None = None) -> AttnBwdArgs:
+    """Build an AttnBwdArgs from raw integer pointers (o may be 0).  strides:
+    {name: (batch, head, seq)} element strides for any of dout, q, k, v, o, dq,
+    dk, dv; absent ones are contiguous."""
     a = AttnBwdArgs()
+    for name, st in (strides or {}).items():
+        if name not in BWD_STRIDE_FIELDS:
+            raise ValueError(f"no stride field for {name!r}")
+        getattr(a, f"{name}_strides")[:] = [int(x) for x in st]
     a.dout, a.q, a.k, a.v, a.o, a.m, a.l = dout, q, k, v, o, m, l
     a.dq, a.dk, a.dv = dq, dk, dv
     a.workspace, a.workspace_bytes = workspace, workspace_bytes

@@ -59,16 +59,18 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dq_kernel(BwdP
     if (row >= (int64_t)p.BH * S) return;   // the whole wave
     const int64_t bh = row / S;
     const int qi = (int)(row - bh * S);
-    const int64_t hoff = bh * S * D;
-    const float *kg = (const float *)p.k + hoff;
-    const float *vg = (const float *)p.v + hoff;
+    const float *kg = bwd_head<const float>(p, p.k, BK, (int)bh);
+    const float *vg = bwd_head<const float>(p, p.v, BV, (int)bh);
+    const int kss = p.ss[BK], vss = p.ss[BV];
+    const float *qr_i = bwd_head<const float>(p, p.q, BQ, (int)bh) + (int64_t)qi * p.ss[BQ];
+    const float *dr_i = bwd_head<const float>(p, p.dout, BDOUT, (int)bh) + (int64_t)qi * p.ss[BDOUT];
 
     float qv[NE], dov[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
         const int d = lane + 64 * e;
-        qv[e] = d < D ? ((const float *)p.q)[row * D + d] : 0.f;
-        dov[e] = d < D ? ((const float *)p.dout)[row * D + d] : 0.f;
+        qv[e] = d < D ? qr_i[d] : 0.f;
+        dov[e] = d < D ? dr_i[d] : 0.f;
     }
     const float m_i = bwd_load_ml<float>(p.m, row, true);
     const float l_i = bwd_load_ml<float>(p.l, row, true);
@@ -80,18 +82,19 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dq_kernel(BwdP
     auto prob = [&](int j0, float &pv, float &dp) __attribute__((always_inline)) {
         const int j = j0 + lane;
         const int jc = j <= last ? j : last;
-        const float s = bwd_f32_dot<D>(qv, kg + (int64_t)jc * D);
-        dp = bwd_f32_dot<D>(dov, vg + (int64_t)jc * D);
+        const float s = bwd_f32_dot<D>(qv, kg + (int64_t)jc * kss);
+        dp = bwd_f32_dot<D>(dov, vg + (int64_t)jc * vss);
         pv = j <= last ? fast_exp2(__builtin_fmaf(s, c, -lse2)) : 0.f;
     };
 
     float drow;
     if (p.o != nullptr) {
+        const float *or_i = bwd_head<const float>(p, p.o, BO, (int)bh) + (int64_t)qi * p.ss[BO];
         float part = 0.f;
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
             const int d = lane + 64 * e;
-            if (d < D) part = __builtin_fmaf(((const float *)p.o)[row * D + d], dov[e], part);
+            if (d < D) part = __builtin_fmaf(or_i[d], dov[e], part);
         }
         drow = bwd_f32_wave_sum(part);
     } else {
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dq_kernel(BwdP
         const int n = min(64, last - j0 + 1);
         for (int jj = 0; jj < n; ++jj) {
             const float dsj = bwd_f32_lane(ds, jj);
-            const float *kr = kg + (int64_t)(j0 + jj) * D;
+            const float *kr = kg + (int64_t)(j0 + jj) * kss;
 #pragma unroll
             for (int e = 0; e < NE; ++e) {
                 const int d = lane + 64 * e;
@@ -126,10 +129,11 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dq_kernel(BwdP
             }
         }
     }
+    float *dq_i = bwd_head<float>(p, p.dq, BDQ, (int)bh) + (int64_t)qi * p.ss[BDQ];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
         const int d = lane + 64 * e;
-        if (d < D) ((float *)p.dq)[row * D + d] = acc[e] * p.scale;
+        if (d < D) dq_i[d] = acc[e] * p.scale;
     }
 }
 
@@ -142,18 +146,20 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dkdv_kernel(Bw
     if (row >= (int64_t)p.BH * S) return;
     const int64_t bh = row / S;
     const int kj = (int)(row - bh * S);
-    const int64_t hoff = bh * S * D;
-    const float *qg = (const float *)p.q + hoff;
-    const float *dog = (const float *)p.dout + hoff;
+    const float *qg = bwd_head<const float>(p, p.q, BQ, (int)bh);
+    const float *dog = bwd_head<const float>(p, p.dout, BDOUT, (int)bh);
+    const int qss = p.ss[BQ], doss = p.ss[BDOUT];
     const float *lse2g = p.lse2 + bh * S;
     const float *drowg = p.drow + bh * S;
+    const float *kr_j = bwd_head<const float>(p, p.k, BK, (int)bh) + (int64_t)kj * p.ss[BK];
+    const float *vr_j = bwd_head<const float>(p, p.v, BV, (int)bh) + (int64_t)kj * p.ss[BV];
 
     float kv[NE], vv[NE];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
         const int d = lane + 64 * e;
-        kv[e] = d < D ? ((const float *)p.k)[row * D + d] : 0.f;
-        vv[e] = d < D ? ((const float *)p.v)[row * D + d] : 0.f;
+        kv[e] = d < D ? kr_j[d] : 0.f;
+        vv[e] = d < D ? vr_j[d] : 0.f;
     }
     const float c = p.scale_log2;
     const int first = CAUSAL ? kj : 0;   // first query that sees key kj
@@ -164,16 +170,16 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dkdv_kernel(Bw
     for (int i0 = first; i0 < S; i0 += 64) {
         const int i = i0 + lane;
         const int ic = i < S ? i : S - 1;
-        const float s = bwd_f32_dot<D>(kv, qg + (int64_t)ic * D);
-        const float dp = bwd_f32_dot<D>(vv, dog + (int64_t)ic * D);
+        const float s = bwd_f32_dot<D>(kv, qg + (int64_t)ic * qss);
+        const float dp = bwd_f32_dot<D>(vv, dog + (int64_t)ic * doss);
         const float pv = i < S ? fast_exp2(__builtin_fmaf(s, c, -lse2g[ic])) : 0.f;
         const float ds = pv * (dp - drowg[ic]);
         const int n = min(64, S - i0);
         for (int ii = 0; ii < n; ++ii) {
             const float pi = bwd_f32_lane(pv, ii);
             const float dsi = bwd_f32_lane(ds, ii);
-            const float *qr = qg + (int64_t)(i0 + ii) * D;
-            const float *dr = dog + (int64_t)(i0 + ii) * D;
+            const float *qr = qg + (int64_t)(i0 + ii) * qss;
+            const float *dr = dog + (int64_t)(i0 + ii) * doss;
 #pragma unroll
             for (int e = 0; e < NE; ++e) {
                 const int d = lane + 64 * e;
@@ -184,12 +190,14 @@ __global__ __launch_bounds__(kBwdF32Waves * 64) void attn_bwd_f32_dkdv_kernel(Bw
             }
         }
     }
+    float *dk_j = bwd_head<float>(p, p.dk, BDK, (int)bh) + (int64_t)kj * p.ss[BDK];
+    float *dv_j = bwd_head<float>(p, p.dv, BDV, (int)bh) + (int64_t)kj * p.ss[BDV];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
         const int d = lane + 64 * e;
         if (d < D) {
-            ((float *)p.dk)[row * D + d] = acc_k[e] * p.scale;
-            ((float *)p.dv)[row * D + d] = acc_v[e];
+            dk_j[d] = acc_k[e] * p.scale;
+            dv_j[d] = acc_v[e];
         }
     }
 }

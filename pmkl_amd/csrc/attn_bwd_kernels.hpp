@@ -36,17 +36,29 @@ namespace pmkl_amd {
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// The [B, H, S, D] tensors of the backward, indexing the stride arrays.
+enum BwdTensor : int { BQ = 0, BK, BV, BO, BDOUT, BDQ, BDK, BDV };
+
 struct BwdParams {
-    const void *q, *k, *v, *o, *dout;   // [BH, S, D] contiguous; o may be null
-    const void *m, *l;                  // [BH, S], the forward's outputs
-    void *dq, *dk, *dv;                 // [BH, S, D]
+    const void *q, *k, *v, *o, *dout;   // [B, H, S, D], head_dim contiguous; o may be null
+    const void *m, *l;                  // [BH, S] contiguous, the forward's outputs
+    void *dq, *dk, *dv;                 // [B, H, S, D]
     float *lse2;                        // workspace [BH, S]: m * log2(e) + log2(l)
     float *drow;                        // workspace [BH, S]: D_n
-    int32_t S, BH;
+    int32_t S, BH, H;
     int32_t n_qtiles, n_ktiles;         // ceil(S / owned rows per workgroup), dq and dk/dv kernels
     float scale, scale_log2;
     int32_t ml_f32;                     // m, l stored as float (else in T)
+    int64_t sb[8], sh[8];               // batch and head element strides, by BwdTensor
+    int32_t ss[8];                      // seq (row) element strides, by BwdTensor
 };
+
+// Row 0 of head bh (= b H + h) of tensor t.
+template <typename T>
+__device__ __forceinline__ T *bwd_head(const BwdParams &p, const void *base, int t, int bh) {
+    const int b = bh / p.H, h = bh - b * p.H;
+    return (T *)base + (int64_t)b * p.sb[t] + (int64_t)h * p.sh[t];
+}
 
 // Waves per workgroup: 8 (two per SIMD) where the registers of a wave fit in
 // 256, else 4 (one per SIMD, up to 512 registers): at head_dim 128 the
@@ -70,13 +82,13 @@ struct BwdTile {
     static constexpr bool PARTIAL = CHUNKS % THREADS != 0;
 };
 
-// Buffer resource of the rows [r0, S) of a [S, D] matrix: rows past S read as
-// zero.
+// Buffer resource of the rows [r0, S) of a [S, D] matrix with row stride ss
+// elements: rows past S read as zero.
 template <typename T, int D>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t bwd_rows_rsrc(const T *base, int r0, int S) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bwd_rows_rsrc(const T *base, int r0, int S, int ss) {
     const int rows = min(64, S - r0);
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (int64_t)r0 * D), (short)0,
-                                             (int)((rows - 1) * D + D) * (int)sizeof(T), 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(base + (int64_t)r0 * ss), (short)0,
+                                             (int)((rows - 1) * ss + D) * (int)sizeof(T), 0x00020000);
 }
 
 // A-operand fragment (rows) of a 32-row block from a tile stored with swz_k:
@@ -144,12 +156,12 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
     const int bh = blockIdx.x % p.BH;
     const int qt = CAUSAL ? p.n_qtiles - 1 - (int)blockIdx.x / p.BH : (int)blockIdx.x / p.BH;
     const int S = p.S;
-    const int64_t hoff = (int64_t)bh * S * D;
-    const T *qg = (const T *)p.q + hoff;
-    const T *kg = (const T *)p.k + hoff;
-    const T *vg = (const T *)p.v + hoff;
-    const T *dog = (const T *)p.dout + hoff;
-    T *dqg = (T *)p.dq + hoff;
+    const T *qg = bwd_head<const T>(p, p.q, BQ, bh);
+    const T *kg = bwd_head<const T>(p, p.k, BK, bh);
+    const T *vg = bwd_head<const T>(p, p.v, BV, bh);
+    const T *dog = bwd_head<const T>(p, p.dout, BDOUT, bh);
+    T *dqg = bwd_head<T>(p, p.dq, BDQ, bh);
+    const int qss = p.ss[BQ], kss = p.ss[BK], vss = p.ss[BV], doss = p.ss[BDOUT];
 
     const int q0 = qt * kBwdRows;
     const int q0w = q0 + 32 * wave;
@@ -164,8 +176,8 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
     frag qf[NDK], df[NDK];
 #pragma unroll
     for (int dk = 0; dk < NDK; ++dk) {
-        qf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(qg + (int64_t)qrow * D + 16 * dk + 8 * hi));
-        df[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(dog + (int64_t)qrow * D + 16 * dk + 8 * hi));
+        qf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(qg + (int64_t)qrow * qss + 16 * dk + 8 * hi));
+        df[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(dog + (int64_t)qrow * doss + 16 * dk + 8 * hi));
     }
     // log2-sum-exp of the row: P = exp2(s * scale * log2(e) - lse2).
     const float m_i = bwd_load_ml<T>(p.m, (int64_t)bh * S + qrow, p.ml_f32 != 0);
@@ -176,20 +188,21 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
     // ---- staging: tile kt lives in LDS stage kt % 3; the registers hold the
     // tile two ahead of the one being computed ----
     u32x4_t kreg[LOADS], vreg[LOADS];
-    int goff[LOADS];
+    int goffk[LOADS], goffv[LOADS];   // lane byte offsets of its chunks in a K / V tile
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         const int sl = j * kBwdThreads + tid;
-        goff[j] = ((sl / CPR) * D + 8 * (sl % CPR)) * (int)sizeof(T);
+        goffk[j] = ((sl / CPR) * kss + 8 * (sl % CPR)) * (int)sizeof(T);
+        goffv[j] = ((sl / CPR) * vss + 8 * (sl % CPR)) * (int)sizeof(T);
     }
     auto gload = [&](int kt) __attribute__((always_inline)) {
-        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S);
-        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S);
+        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S, kss);
+        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S, vss);
 #pragma unroll
         for (int j = 0; j < LOADS; ++j)
             if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
-                kreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[j], 0, 0));
-                vreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[j], 0, 0));
+                kreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goffk[j], 0, 0));
+                vreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goffv[j], 0, 0));
             }
     };
     auto swrite = [&](int st) __attribute__((always_inline)) {
@@ -209,13 +222,13 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
     u32x4_t kreg2[2][LOADS], vreg2[2][LOADS];
     auto gload2 = [&](int kt, auto set_c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
-        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S);
-        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S);
+        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S, kss);
+        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S, vss);
 #pragma unroll
         for (int j = 0; j < LOADS; ++j)
             if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
-                kreg2[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[j], 0, 0));
-                vreg2[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[j], 0, 0));
+                kreg2[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goffk[j], 0, 0));
+                vreg2[SET][j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goffv[j], 0, 0));
             }
     };
     auto swrite2 = [&](int st, auto set_c) __attribute__((always_inline)) {
@@ -431,11 +444,11 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
 
     if (p.o != nullptr) {
         // D_n = dout_n . o_n straight from O (same lane split as the fragments)
-        const T *og = (const T *)p.o + hoff;
+        const T *og = bwd_head<const T>(p, p.o, BO, bh);
         float part = 0.f;
 #pragma unroll
         for (int dk = 0; dk < NDK; ++dk) {
-            const frag of = __builtin_bit_cast(frag, *(const u32x4_t *)(og + (int64_t)qrow * D + 16 * dk + 8 * hi));
+            const frag of = __builtin_bit_cast(frag, *(const u32x4_t *)(og + (int64_t)qrow * p.ss[BO] + 16 * dk + 8 * hi));
 #pragma unroll
             for (int e = 0; e < 8; ++e) part = __builtin_fmaf((float)of[e], (float)df[dk][e], part);
         }
@@ -454,7 +467,7 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
 
     // ---- epilogue: dq = scale * dQ^T, lane = query column ----
     if (wave_active && qi < S) {
-        T *row = dqg + (int64_t)qi * D;
+        T *row = dqg + (int64_t)qi * p.ss[BDQ];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -503,15 +516,15 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
     const int bh = blockIdx.x % p.BH;
     const int ktile = (int)blockIdx.x / p.BH;
     const int S = p.S;
-    const int64_t hoff = (int64_t)bh * S * D;
-    const T *qg = (const T *)p.q + hoff;
-    const T *kg = (const T *)p.k + hoff;
-    const T *vg = (const T *)p.v + hoff;
-    const T *dog = (const T *)p.dout + hoff;
+    const T *qg = bwd_head<const T>(p, p.q, BQ, bh);
+    const T *kg = bwd_head<const T>(p, p.k, BK, bh);
+    const T *vg = bwd_head<const T>(p, p.v, BV, bh);
+    const T *dog = bwd_head<const T>(p, p.dout, BDOUT, bh);
     const float *lse2g = p.lse2 + (int64_t)bh * S;
     const float *drowg = p.drow + (int64_t)bh * S;
-    T *dkg = (T *)p.dk + hoff;
-    T *dvg = (T *)p.dv + hoff;
+    T *dkg = bwd_head<T>(p, p.dk, BDK, bh);
+    T *dvg = bwd_head<T>(p, p.dv, BDV, bh);
+    const int qss = p.ss[BQ], doss = p.ss[BDOUT];
 
     const int k0 = ktile * kBwdRows;
     const int k0w = k0 + 32 * wave;
@@ -526,28 +539,29 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
     frag kf[NDK], vf[NDK];
 #pragma unroll
     for (int dk = 0; dk < NDK; ++dk) {
-        kf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(kg + (int64_t)krow * D + 16 * dk + 8 * hi));
-        vf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(vg + (int64_t)krow * D + 16 * dk + 8 * hi));
+        kf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(kg + (int64_t)krow * p.ss[BK] + 16 * dk + 8 * hi));
+        vf[dk] = __builtin_bit_cast(frag, *(const u32x4_t *)(vg + (int64_t)krow * p.ss[BV] + 16 * dk + 8 * hi));
     }
     const float c = p.scale_log2;
 
     // ---- staging of Q, dout (two layouts each) and the row vectors ----
     u32x4_t qreg[LOADS], oreg[LOADS];
     float vreg;      // one row-vector element per thread (threads 0..127)
-    int goff[LOADS];
+    int goffq[LOADS], goffo[LOADS];   // lane byte offsets of its chunks in a Q / dout tile
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         const int sl = j * kBwdThreads + tid;
-        goff[j] = ((sl / CPR) * D + 8 * (sl % CPR)) * (int)sizeof(T);
+        goffq[j] = ((sl / CPR) * qss + 8 * (sl % CPR)) * (int)sizeof(T);
+        goffo[j] = ((sl / CPR) * doss + 8 * (sl % CPR)) * (int)sizeof(T);
     }
     auto gload = [&](int qtl) __attribute__((always_inline)) {
-        const auto qr = bwd_rows_rsrc<T, D>(qg, qtl * BN, S);
-        const auto orr = bwd_rows_rsrc<T, D>(dog, qtl * BN, S);
+        const auto qr = bwd_rows_rsrc<T, D>(qg, qtl * BN, S, qss);
+        const auto orr = bwd_rows_rsrc<T, D>(dog, qtl * BN, S, doss);
 #pragma unroll
         for (int j = 0; j < LOADS; ++j)
             if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
-                qreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qr, goff[j], 0, 0));
-                oreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(orr, goff[j], 0, 0));
+                qreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(qr, goffq[j], 0, 0));
+                oreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(orr, goffo[j], 0, 0));
             }
         if (tid < 2 * BN) {
             const int row = qtl * BN + (tid & (BN - 1));
@@ -779,8 +793,8 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
 
     // ---- epilogue: dk = scale * dK^T, dv = dV^T; lane = key column ----
     if (wave_active && kj < S) {
-        T *rk = dkg + (int64_t)kj * D;
-        T *rv = dvg + (int64_t)kj * D;
+        T *rk = dkg + (int64_t)kj * p.ss[BDK];
+        T *rv = dvg + (int64_t)kj * p.ss[BDV];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll

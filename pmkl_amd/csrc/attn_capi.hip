@@ -240,6 +240,14 @@ BwdKernels select_bwd(int32_t dt, int64_t d, bool causal) {
     return {nullptr, nullptr, 0, 0, 0, 0, false};
 }
 
+// One [B, H, S, D] tensor of a backward call, for the checks and the launch.
+struct BwdTensorArg {
+    const char *name;
+    const void *ptr;
+    const int64_t *strides;
+    bool optional;   // may be null (o)
+};
+
 // Validates a backward call except for the workspace.  *empty is set for a
 // problem with no rows (nothing to launch).
 int check_bwd(const pmkl_attn_bwd_args *a, bool *empty) {
@@ -261,16 +269,19 @@ int check_bwd(const pmkl_attn_bwd_args *a, bool *empty) {
     PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
                  (long long)(B * H), (long long)S);
     PMKL_REQUIRE(B * H * S * D < (1LL << 62), PMKL_EINVAL, "tensors span too many elements");
-    const struct {
-        const char *name;
-        const void *ptr;
-    } tensors[] = {{"dout", a->dout}, {"q", a->q}, {"k", a->k}, {"v", a->v}, {"dq", a->dq}, {"dk", a->dk},
-                   {"dv", a->dv}};
+    const size_t es = dtype_size(a->dtype);
+    const BwdTensorArg tensors[] = {
+        {"dout", a->dout, a->dout_strides, false}, {"q", a->q, a->q_strides, false},
+        {"k", a->k, a->k_strides, false},          {"v", a->v, a->v_strides, false},
+        {"o", a->o, a->o_strides, true},           {"dq", a->dq, a->dq_strides, false},
+        {"dk", a->dk, a->dk_strides, false},       {"dv", a->dv, a->dv_strides, false}};
+    int rc;
     for (const auto &t : tensors) {
-        PMKL_REQUIRE(t.ptr != nullptr, PMKL_EINVAL, "%s is a null pointer", t.name);
-        PMKL_REQUIRE(((uintptr_t)t.ptr % 16) == 0, PMKL_EINVAL, "%s must be 16-byte aligned", t.name);
+        if (t.ptr == nullptr && t.optional) continue;
+        int64_t st[3];
+        default_strides(st, t.strides, H, S, D);
+        if ((rc = check_tensor(t.name, t.ptr, st, B, H, S, D, es)) != PMKL_OK) return rc;
     }
-    PMKL_REQUIRE(a->o == nullptr || ((uintptr_t)a->o % 16) == 0, PMKL_EINVAL, "o must be 16-byte aligned");
     PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
     const size_t ml_es = dtype_size(a->ml_dtype);
     PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
@@ -312,6 +323,25 @@ int launch_bwd(const pmkl_attn_bwd_args *a, float *ws, void *stream) {
     p.drow = ws + B * H * S;
     p.S = (int32_t)S;
     p.BH = (int32_t)(B * H);
+    p.H = (int32_t)H;
+    {
+        const int64_t *in[8];
+        in[pmkl_amd::BQ] = a->q_strides;
+        in[pmkl_amd::BK] = a->k_strides;
+        in[pmkl_amd::BV] = a->v_strides;
+        in[pmkl_amd::BO] = a->o_strides;
+        in[pmkl_amd::BDOUT] = a->dout_strides;
+        in[pmkl_amd::BDQ] = a->dq_strides;
+        in[pmkl_amd::BDK] = a->dk_strides;
+        in[pmkl_amd::BDV] = a->dv_strides;
+        for (int t = 0; t < 8; ++t) {
+            int64_t st[3];
+            default_strides(st, in[t], H, S, D);
+            p.sb[t] = st[0];
+            p.sh[t] = st[1];
+            p.ss[t] = (int32_t)st[2];   // a 64-row tile spans < 2 GiB (checked)
+        }
+    }
     p.n_qtiles = (int32_t)nq;
     p.n_ktiles = (int32_t)nk;
     p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);

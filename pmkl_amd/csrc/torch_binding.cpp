@@ -229,7 +229,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_bw(const at:
                                                                        const at::Tensor &out_m,
                                                                        const at::Tensor &out_l, bool is_causal) {
     TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "Input tensor shapes must match");
-    TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(), "Input tensor must be contiguous");
+    // The CPU body indexes contiguous rows, as the reference's does (its check
+    // and message, fused_self_attention.cpp:181-182); the device backward takes
+    // any strides with head_dim contiguous, without copies.
+    TORCH_CHECK(!q.is_cpu() || (q.is_contiguous() && k.is_contiguous() && v.is_contiguous()),
+                "Input tensor must be contiguous");
     TORCH_CHECK(q.sizes() == k.sizes() && q.sizes() == v.sizes(), "Input tensor shapes must match");
     TORCH_CHECK(dout.sizes() == q.sizes(), "dout must have the shape of q");
     const int64_t B = q.size(0), H = q.size(1), S = q.size(2), D = q.size(3);
@@ -244,12 +248,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_bw(const at:
                     out_m.device() == q.device() && out_l.device() == q.device(),
                 "Input tensors must be on one device");
 
-    auto dq = at::zeros_like(q);
-    auto dk = at::zeros_like(k);
-    auto dv = at::zeros_like(v);
-    auto doc = dout.contiguous();
-
     if (q.is_cpu()) {
+        auto dq = at::zeros_like(q);
+        auto dk = at::zeros_like(k);
+        auto dv = at::zeros_like(v);
+        auto doc = dout.contiguous();
         AT_DISPATCH_FLOATING_TYPES_AND2(at::ScalarType::Half, at::ScalarType::BFloat16, v.scalar_type(),
                                         "fused_self_attention_bw", [&]() {
                                             auto mc = out_m.contiguous().to(v.scalar_type());
@@ -269,6 +272,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_bw(const at:
     const int32_t dt = to_pmkl_dtype(q.scalar_type());
     TORCH_CHECK(pmkl_attn_bwd_supported(dt, D), "fused_self_attention_bw: the device backward supports float32, ",
                 "float16 and bfloat16 with head_dim 32, 64 or 128, got ", q.scalar_type(), " head_dim ", D);
+    // Gradients come back contiguous [B, H, S, D]; the kernels write every element.
+    auto gopts = q.options().memory_format(at::MemoryFormat::Contiguous);
+    auto dq = at::empty({B, H, S, D}, gopts);
+    auto dk = at::empty({B, H, S, D}, gopts);
+    auto dv = at::empty({B, H, S, D}, gopts);
     if (B * H * S == 0) return std::forward_as_tuple(dq, dk, dv);
     const int32_t mdt = to_pmkl_dtype(out_m.scalar_type());
     TORCH_CHECK(out_m.scalar_type() == out_l.scalar_type() && (mdt == dt || mdt == PMKL_DTYPE_F32),
@@ -276,14 +284,25 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> fused_self_attention_bw(const at:
 
     c10::OptionalDeviceGuard guard(q.device());
     auto mc = out_m.contiguous(), lc = out_l.contiguous();
+    // Strided views go to the kernels as they are; only a layout the kernels
+    // cannot address (head_dim not contiguous, strides or base not 16-byte
+    // aligned) is copied.
+    auto qd = device_view(q), kd = device_view(k), vd = device_view(v), dod = device_view(dout);
     const uint64_t ws_bytes = pmkl_attn_bwd_workspace_size(B, H, S);
     auto ws = at::empty({(int64_t)((ws_bytes + 3) / 4)}, q.options().dtype(at::kFloat));
     pmkl_attn_bwd_args a;
     std::memset(&a, 0, sizeof(a));
-    a.dout = doc.data_ptr();
-    a.q = q.data_ptr();
-    a.k = k.data_ptr();
-    a.v = v.data_ptr();
+    a.dout = dod.data_ptr();
+    a.q = qd.data_ptr();
+    a.k = kd.data_ptr();
+    a.v = vd.data_ptr();
+    fill_strides(a.dout_strides, dod);
+    fill_strides(a.q_strides, qd);
+    fill_strides(a.k_strides, kd);
+    fill_strides(a.v_strides, vd);
+    fill_strides(a.dq_strides, dq);
+    fill_strides(a.dk_strides, dk);
+    fill_strides(a.dv_strides, dv);
     a.o = nullptr;
     a.m = mc.data_ptr();
     a.l = lc.data_ptr();

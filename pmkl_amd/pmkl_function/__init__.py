@@ -50,10 +50,13 @@ class fused_self_attention_(Function):
         if q.is_cuda:
             if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
                 raise NotImplementedError(f"the device backward supports float32, float16 and bfloat16, got {q.dtype}")
-            from .. import attn_bwd
+            from .. import attn_bwd, kernel_view
 
-            dq, dk, dv = attn_bwd(grad_output.contiguous(), q.contiguous(), k.contiguous(), v.contiguous(),
-                                  out_m, out_l, is_causal=ctx.is_casual, out=out)
+            # Strided inputs (BSHD views, a packed QKV) go to the kernels as
+            # they are; only what they cannot address (an expanded gradient,
+            # say) is made contiguous.
+            dq, dk, dv = attn_bwd(kernel_view(grad_output), kernel_view(q), kernel_view(k), kernel_view(v),
+                                  out_m, out_l, is_causal=ctx.is_casual, out=kernel_view(out))
         elif q.is_cpu and ctx.debug:
             dq, dk, dv = pmkl_pytorch_ext.fused_self_attention_bw(grad_output, q, k, v, out_m, out_l, ctx.is_casual)
         else:

@@ -204,3 +204,80 @@ def test_bwd_torch_operator_and_autograd_device(device, dtype):
     ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), mn, ln, causal=True)
     fl = _term_floors(r(q), r(k), r(v), r(do), mn, ln, True) if dtype == "fp32" else (0.0, 0.0, 0.0)
     _check([r(qg.grad), r(kg.grad), r(vg.grad)], ref, dtype, f"autograd device {dtype}", fl)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_bwd_strided_views_without_copies(device, dtype, D):
+    """Strided inputs and outputs of the backward, as the forward takes them:
+    q and k are views into one packed [B, S, 3, H, D] buffer, v, dout and o
+    are BSHD views (so K and V have different row strides), and dq, dk, dv are
+    written into BSHD buffers through the C ABI.  The kernels do the same
+    arithmetic whatever the strides, so every gradient equals the contiguous
+    call's bit for bit; the contiguous call is held to the oracle.  The torch
+    operator and the autograd entry take the same views (no copies on their
+    way to the kernels) and give the same bits."""
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd import capi, pmkl_pytorch_ext
+    from pmkl_amd.pmkl_function import fused_self_attention
+    from pmkl_amd.workloads import small_inputs, torch_dtype
+
+    B, H, S, causal = 2, 3, 190, True
+    tag = f"bwd strided {dtype} D={D} B{B} H{H} S{S}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=700 + D)
+    rng = np.random.Generator(np.random.PCG64(701 + D))
+    do = torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to(torch_dtype(dtype))
+    dev = torch.device("cuda:0")
+    tdt = torch_dtype(dtype)
+    qkv = torch.zeros((B, S, 3, H, D), dtype=tdt, device=dev)
+    qkv[:, :, 0] = q.transpose(1, 2).to(dev)
+    qkv[:, :, 1] = k.transpose(1, 2).to(dev)
+    qs, ks = qkv[:, :, 0].transpose(1, 2), qkv[:, :, 1].transpose(1, 2)
+    bshd = lambda t: t.transpose(1, 2).contiguous().to(dev).transpose(1, 2)
+    vs, dos = bshd(v), bshd(do)
+    assert qs.stride(2) == 3 * H * D and vs.stride(2) == H * D and not qs.is_contiguous()
+    obuf = torch.empty((B, S, H, D), dtype=tdt, device=dev)
+    os_ = obuf.transpose(1, 2)
+    o, m, l = pmkl_amd.attn_fwd(qs, ks, vs, is_causal=causal, out=os_)
+
+    qc, kc, vc, doc, oc = (x.contiguous() for x in (qs, ks, vs, dos, os_))
+    want = pmkl_amd.attn_bwd(doc, qc, kc, vc, m, l, is_causal=causal, out=oc)
+
+    # C ABI with strided inputs and outputs
+    gb = [torch.full((B, S, H, D), float("nan"), dtype=tdt, device=dev) for _ in range(3)]
+    gv = [g.transpose(1, 2) for g in gb]
+    ws_bytes = int(capi.load().pmkl_attn_bwd_workspace_size(B, H, S))
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+    st = lambda t: tuple(t.stride()[:3])
+    a = capi.make_bwd_args(dos.data_ptr(), qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), os_.data_ptr(),
+                           m.data_ptr(), l.data_ptr(), gv[0].data_ptr(), gv[1].data_ptr(), gv[2].data_ptr(),
+                           ws.data_ptr(), ws.numel() * 4, dtype=pmkl_amd.torch_dtype_to_pmkl(tdt),
+                           batch=B, heads=H, seq_len=S, head_dim=D, is_causal=causal,
+                           strides={"dout": st(dos), "q": st(qs), "k": st(ks), "v": st(vs), "o": st(os_),
+                                    "dq": st(gv[0]), "dk": st(gv[1]), "dv": st(gv[2])})
+    assert capi.attn_bwd_raw(a, torch.cuda.current_stream().cuda_stream) == capi.PMKL_OK, capi.last_error()
+    # the Python wrapper with strided inputs (contiguous outputs)
+    got_py = pmkl_amd.attn_bwd(dos, qs, ks, vs, m, l, is_causal=causal, out=os_)
+    # the torch operator (no O: its own row-term pass) against the contiguous call without O
+    want_no_o = pmkl_amd.attn_bwd(doc, qc, kc, vc, m, l, is_causal=causal)
+    got_op = pmkl_pytorch_ext.fused_self_attention_bw(dos, qs, ks, vs, m, l, causal)
+    # autograd through strided leaves
+    qb, kb2, vb = (x.transpose(1, 2).detach().clone().requires_grad_(True) for x in (qs, ks, vs))
+    out, _, _ = fused_self_attention(qb.transpose(1, 2), kb2.transpose(1, 2), vb.transpose(1, 2), causal)
+    out.backward(dos)
+    torch.cuda.synchronize()
+    for name, w, g1, g2, g3, w0, g4 in zip(("dq", "dk", "dv"), want, gv, got_py, got_op, want_no_o,
+                                           (qb.grad, kb2.grad, vb.grad)):
+        assert torch.equal(g1, w), f"{tag}: C ABI strided {name} differs from the contiguous call"
+        assert torch.equal(g2, w), f"{tag}: attn_bwd strided {name} differs"
+        assert torch.equal(g3, w0), f"{tag}: torch op strided {name} differs"
+        assert torch.equal(g4.transpose(1, 2), w), f"{tag}: autograd strided {name} differs"
+    r = lambda t: _np(t).reshape(B * H, S, D)
+    ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), _np(m).reshape(B * H, S), _np(l).reshape(B * H, S),
+                          causal=causal)
+    fl = _term_floors(r(q), r(k), r(v), r(do), _np(m).reshape(B * H, S), _np(l).reshape(B * H, S), causal) \
+        if dtype == "fp32" else (0.0, 0.0, 0.0)
+    _say(f"  {_check([r(x) for x in want], ref, dtype, tag, fl)}")

@@ -40,7 +40,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_abi_version_and_support_matrix():
     lib = capi.load()
-    assert lib.pmkl_abi_version() == 3
+    assert lib.pmkl_abi_version() == 4
     for dt in (capi.PMKL_DTYPE_F32, capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
         for d in (32, 64, 128):
             assert lib.pmkl_attn_fwd_supported(dt, d) == 1
@@ -102,27 +102,29 @@ def test_flat_entry_point_validates_like_the_template():
     assert rc == capi.PMKL_EINVAL and "null pointer" in capi.last_error()
 
 
-def test_args_struct_layout_matches_header(tmp_path):
-    """Field offsets and size of the ctypes mirror equal those of the C struct,
-    as a C compiler lays it out from include/pmkl_attn.h."""
+@pytest.mark.parametrize("cname,cls", [("pmkl_attn_fwd_args", "AttnFwdArgs"), ("pmkl_attn_bwd_args", "AttnBwdArgs")])
+def test_args_struct_layout_matches_header(tmp_path, cname, cls):
+    """Field offsets and size of the ctypes mirrors equal those of the C
+    structs, as a C compiler lays them out from include/pmkl_attn.h."""
     import shutil
     import subprocess
 
     cc = shutil.which("gcc") or shutil.which("cc")
     if cc is None:
         pytest.skip("no C compiler")
-    fields = [f[0] for f in capi.AttnFwdArgs._fields_]
+    mirror = getattr(capi, cls)
+    fields = [f[0] for f in mirror._fields_]
     src = tmp_path / "layout.c"
-    body = "".join(f'  printf("%s %zu\\n", "{f}", offsetof(pmkl_attn_fwd_args, {f}));\n' for f in fields)
+    body = "".join(f'  printf("%s %zu\\n", "{f}", offsetof({cname}, {f}));\n' for f in fields)
     src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "pmkl_attn.h"\nint main(void) {\n'
-                   + body + '  printf("sizeof %zu\\n", sizeof(pmkl_attn_fwd_args));\n  return 0;\n}\n')
+                   + body + f'  printf("sizeof %zu\\n", sizeof({cname}));\n  return 0;\n}}\n')
     exe = tmp_path / "layout"
     subprocess.run([cc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
     out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
                                                          check=True).stdout.splitlines())
     for f in fields:
-        assert int(out[f]) == getattr(capi.AttnFwdArgs, f).offset, f
-    assert int(out["sizeof"]) == ctypes.sizeof(capi.AttnFwdArgs)
+        assert int(out[f]) == getattr(mirror, f).offset, f
+    assert int(out["sizeof"]) == ctypes.sizeof(mirror)
 
 
 def _bwd_args(**kw):
@@ -166,6 +168,14 @@ def test_bwd_error_paths():
     _expect_bwd(_bwd_args(l=0), capi.PMKL_EINVAL, "m / l must not be null")
     _expect_bwd(_bwd_args(workspace=0), capi.PMKL_EINVAL, "workspace must be")
     _expect_bwd(_bwd_args(workspace_bytes=100), capi.PMKL_EINVAL, "workspace of 100 bytes is too small")
+    # strides: validated per tensor, as the forward's
+    _expect_bwd(_bwd_args(strides={"v": (2 * 64 * 64, 64 * 64, 60)}), capi.PMKL_EINVAL,
+                r"v strides \(8192, 4096, 60\) must be non-negative with seq stride >= head_dim 64")
+    _expect_bwd(_bwd_args(strides={"dq": (2 * 64 * 72, 72, 2 * 72 + 4)}), capi.PMKL_EINVAL,
+                r"dq strides .* must be multiples of 8 elements")
+    _expect_bwd(_bwd_args(strides={"dout": (-1, 64, 128)}), capi.PMKL_EINVAL, "dout strides")
+    with pytest.raises(ValueError, match="no stride field"):
+        _bwd_args(strides={"m": (0, 0, 1)})
     # an empty problem succeeds without touching anything
     assert capi.attn_bwd_raw(_bwd_args(seq_len=0, dq=0, workspace=0)) == capi.PMKL_OK
 
