@@ -123,6 +123,19 @@ __device__ __forceinline__ float w64_mask_key(float s, int d) {
     asm volatile("v_cmp_le_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %3, %0, vcc" : "+v"(s) : "n"(R), "v"(d), "v"(-INFINITY) : "vcc");
     return s;
 }
+// Row-max steps as single instructions: fmaxf on MFMA results (opaque to the
+// compiler) is lowered with a canonicalising v_max of each input first, 8
+// extra VALU instructions per 32x64 score tile.
+__device__ __forceinline__ float w64_max3(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float w64_max(float a, float b) {
+    float d;
+    asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
 // f(integral_constant<int, I>) for I = B .. E-1, unrolled at compile time.
 template <int B, int E, typename F>
 __device__ __forceinline__ void w64_static_for(F &&f) {
@@ -249,7 +262,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
     constexpr int NSLOT = Sch::NSLOT, RING = Sch::RING;
     static_assert(TILE_CHUNKS % NT == 0, "tile must split evenly over the workgroup's threads");
 
-    __shared__ __attribute__((aligned(1024))) T smem[6][BN * D];   // K slots 0-2, V slots 3-5
+    // LDS slots: tile x of the stream (K and V) lives in slot x % NSL.  Four
+    // slots, so that with NSL-aligned item lengths every item starts at slot
+    // 0 and score set 0, and the unrolled loop below addresses the slots with
+    // compile-time offsets.
+    constexpr int NSL = 4;
+    __shared__ __attribute__((aligned(1024))) T smem[2 * NSL][BN * D];   // K slots 0..NSL-1, V slots NSL..2 NSL-1
     const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) T *)smem[0];
 
     const int tid = threadIdx.x;
@@ -280,7 +298,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     };
 
     // Current item.
-    int bh = 0, qt = 0, q0w = 0, nt = 1, nt2 = 2, ntw = 0;
+    int bh = 0, qt = 0, q0w = 0, nt = 1, npos = NSL, ntw = 0;
     bool wave_active = false;
     const T *kg = nullptr, *vg = nullptr;
     // Next item: its first tiles are loaded during the current item's last
@@ -302,7 +320,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
         map_index<CAUSAL>(p, L, bh, qt);
         q0w = qt * kBlockM + wave_row;    // first row of the wave
         nt = item_tiles(qt);
-        nt2 = (nt + 1) & ~1;              // iterations run by every wave
+        npos = (nt + NSL - 1) & ~(NSL - 1);   // stream positions of the item, run by every wave
         wave_active = q0w < S;
         // Tiles this wave computes: 0 .. ntw-1; only tile ntw-1 can hold keys
         // past a row of the wave (causal diagonal) or past S.
@@ -366,28 +384,29 @@ void attn_fwd_w64_kernel(AttnParams p) {
     const int v_tile_bytes = (int)(BN * p.v_ss * sizeof(T));
     const unsigned lds_w = lds0 + (unsigned)(wave * 1024);
     // DMA j of the K / V tile at stream position kt of the current item into
-    // LDS slot sl (= position % 3, kept by the caller).  Positions past the
-    // item's iterations (nt2) are the next item's tiles 0, 1, 2; tiles are
-    // clamped to the item's last one (the copies past it are never read).
+    // LDS slot sl (= kt % NSL, passed by the caller).  Positions past the
+    // item's own (npos) are the next item's tiles 0, 1, 2; tiles are clamped
+    // to the item's last one (the copies past it are never read).
     auto dma_k = [&](int kt, int sl, int j) __attribute__((always_inline)) {
-        const bool nx = has_next && kt >= nt2;
+        const bool nx = has_next && kt >= npos;
         const T *base = nx ? kg_n : kg;
-        const int tile = nx ? min(kt - nt2, nt_n - 1) : min(kt, nt - 1);
+        const int tile = nx ? min(kt - npos, nt_n - 1) : min(kt, nt - 1);
         w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, k_records, 0x00020000),
                       koff[j] + tile * k_tile_bytes, lds_w + (unsigned)(sl * TILE_BYTES + j * 16 * NT));
     };
     auto dma_v = [&](int kt, int sl, int j) __attribute__((always_inline)) {
-        const bool nx = has_next && kt >= nt2;
+        const bool nx = has_next && kt >= npos;
         const T *base = nx ? vg_n : vg;
-        const int tile = nx ? min(kt - nt2, nt_n - 1) : min(kt, nt - 1);
+        const int tile = nx ? min(kt - npos, nt_n - 1) : min(kt, nt - 1);
         w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, v_records, 0x00020000),
-                      voff[j] + tile * v_tile_bytes, lds_w + (unsigned)((3 + sl) * TILE_BYTES + j * 16 * NT));
+                      voff[j] + tile * v_tile_bytes, lds_w + (unsigned)((NSL + sl) * TILE_BYTES + j * 16 * NT));
     };
-    // DMA i of iteration t: K(t+3) into slot t % 3 (sl0), then V(t+2) into
-    // slot (t+2) % 3 (sl2).
-    auto dma_step = [&](int t, int sl0, int sl2, int i) __attribute__((always_inline)) {
-        if (i < LOADS) dma_k(t + 3, sl0, i);
-        else dma_v(t + 2, sl2, i - LOADS);
+    // DMA i of iteration t: K(t+3) into slot (t+3) % NSL (slk), then V(t+2)
+    // into slot (t+2) % NSL (slv).  The slots hold K(t-1) and V(t-2), last
+    // read before the previous iteration's barrier.
+    auto dma_step = [&](int t, int slk, int slv, int i) __attribute__((always_inline)) {
+        if (i < LOADS) dma_k(t + 3, slk, i);
+        else dma_v(t + 2, slv, i - LOADS);
     };
     // Wait until only the DMAs of the current iteration (2 * LOADS) may be in
     // flight and the wave's LDS reads have returned, then barrier.
@@ -512,9 +531,18 @@ void attn_fwd_w64_kernel(AttnParams p) {
         constexpr int SET = decltype(set_c)::value;
         if (k < 4 * QB) {
             const int qb = k >> 2, kb = (k >> 1) & 1, r0 = 8 * (k & 1);
-            float m = (k & 3) == 0 ? sc[SET][qb][0][0] : mx[qb];
+            const auto &sv = sc[SET][qb][kb];
+            float m;
+            if ((k & 3) == 0) {   // first unit of the block: 8 values, 4 instructions
+                m = w64_max3(sv[r0], sv[r0 + 1], sv[r0 + 2]);
+                m = w64_max3(m, sv[r0 + 3], sv[r0 + 4]);
+                m = w64_max3(m, sv[r0 + 5], sv[r0 + 6]);
+                m = w64_max(m, sv[r0 + 7]);
+            } else {
+                m = mx[qb];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) m = fmaxf(m, sc[SET][qb][kb][r0 + r]);
+                for (int r = 0; r < 8; r += 2) m = w64_max3(m, sv[r0 + r], sv[r0 + r + 1]);
+            }
             asm volatile("" : "+v"(m));
             mx[qb] = m;
         } else if (k < 5 * QB) {
@@ -579,16 +607,19 @@ void attn_fwd_w64_kernel(AttnParams p) {
     };
 
     frag ring[RING];
-    // Iteration t (tile scores in set SET = t & 1): QK of tile t+1 into set
-    // SET ^ 1 and PV of tile t, with the VALU work of the schedule.  LDS
-    // slots: sl0 = t % 3, sl1 = (t+1) % 3, sl2 = (t+2) % 3.
-    auto iteration = [&](int t, auto set_c, int sl0, int sl1, int sl2) __attribute__((always_inline)) {
-        constexpr int SET = decltype(set_c)::value;
+    // Iteration t (PH = t % NSL, tile scores in set SET = t & 1): QK of tile
+    // t+1 into set SET ^ 1 and PV of tile t, with the VALU work of the
+    // schedule.  LDS slots, compile-time: V(t) in PH, K(t+1) in PH + 1, K(t+2)
+    // (the next iteration's first fragments) in PH + 2 (mod NSL).
+    auto iteration = [&](int t, auto ph_c) __attribute__((always_inline)) {
+        constexpr int PH = decltype(ph_c)::value;
+        constexpr int SET = PH & 1;
+        constexpr int SL0 = PH, SL1 = (PH + 1) % NSL, SL2 = (PH + 2) % NSL, SL3 = (PH + 3) % NSL;
         using NSET = std::integral_constant<int, SET ^ 1>;
         using CSET = std::integral_constant<int, SET>;
-        const uint32_t kcur = k_slot_base(sl1);
-        const uint32_t knext = k_slot_base(sl2);
-        const T *Vs = smem[3 + sl0];
+        const uint32_t kcur = k_slot_base(SL1);
+        const uint32_t knext = k_slot_base(SL2);
+        const T *Vs = smem[NSL + SL0];
         w64_static_for<0, NSLOT>([&](auto s_c) __attribute__((always_inline)) {
             constexpr int s = decltype(s_c)::value;
             constexpr int kd = Sch::kind(s), qb = Sch::qb_of(s);
@@ -618,7 +649,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
             }
             w64_static_for<0, 2 * LOADS>([&](auto j_c) __attribute__((always_inline)) {
                 constexpr int j = decltype(j_c)::value;
-                if constexpr (Sch::dma_slot(j, 2 * LOADS) == s) dma_step(t, sl0, sl2, j);
+                if constexpr (Sch::dma_slot(j, 2 * LOADS) == s) dma_step(t, SL3, SL2, j);
             });
             if constexpr (s == Sch::MS0) {
                 w64_mfma_drain();   // the QK MFMAs of tile t+1 have written the scores
@@ -708,16 +739,13 @@ void attn_fwd_w64_kernel(AttnParams p) {
         dma_v(1, 1, j);
     }
     sync_tiles();
-    // LDS slots of stream positions t, t+1, t+2 of the current item; the
-    // stream runs on from item to item.
-    int sa = 0, sb = 1, sc3 = 2;
 
     while (true) {
         pin_q();
-        // Scores and maxima of tile 0 (slot sa; landed, see above).
+        // Scores and maxima of tile 0 (slot 0; landed, see above).
         reset_state();
         {
-            const uint32_t k0 = k_slot_base(sa);
+            const uint32_t k0 = k_slot_base(0);
 #pragma unroll
             for (int f = 0; f < NKF; ++f) {
                 const frag a = kfrag(k0, f);
@@ -738,42 +766,31 @@ void attn_fwd_w64_kernel(AttnParams p) {
             for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
             apply_rescale();
         }
-        sync_tiles();   // every wave is done with K slot sa before iteration 0 refills it
+        sync_tiles();   // every wave is done with K(0) before its slot is refilled
         {
-            const uint32_t k1 = k_slot_base(sb);
+            const uint32_t k1 = k_slot_base(1);
 #pragma unroll
             for (int f = 0; f < RING; ++f) ring[f] = kfrag(k1, f);
         }
 
-        // ---- tiles the wave computes, two per iteration (score sets 0, 1),
-        // an odd last one alone ----
+        // ---- tiles the wave computes, NSL per loop iteration (phases 0..3:
+        // score sets 0, 1, 0, 1 and the LDS slots as compile-time offsets) ----
         int t = 0;
         while (t < ntw) {
-            iteration(t, S0{}, sa, sb, sc3);
-            if (t + 1 == ntw) {
-                const int tmp = sa;
-                sa = sb;
-                sb = sc3;
-                sc3 = tmp;
-                ++t;
-                break;
-            }
-            iteration(t + 1, S1{}, sb, sc3, sa);
-            const int tmp = sa;
-            sa = sc3;
-            sc3 = sb;
-            sb = tmp;
-            t += 2;
+            iteration(t, std::integral_constant<int, 0>{});
+            if (++t == ntw) break;
+            iteration(t, std::integral_constant<int, 1>{});
+            if (++t == ntw) break;
+            iteration(t, std::integral_constant<int, 2>{});
+            if (++t == ntw) break;
+            iteration(t, std::integral_constant<int, 3>{});
+            ++t;
         }
-        // ---- remaining tiles of the item: DMAs and barriers only ----
-        for (; t < nt2; ++t) {
+        // ---- remaining positions of the item: DMAs and barriers only ----
+        for (; t < npos; ++t) {
 #pragma unroll
-            for (int i = 0; i < 2 * LOADS; ++i) dma_step(t, sa, sc3, i);
+            for (int i = 0; i < 2 * LOADS; ++i) dma_step(t, (t + 3) % NSL, (t + 2) % NSL, i);
             sync_tiles();
-            const int tmp = sa;
-            sa = sb;
-            sb = sc3;
-            sc3 = tmp;
         }
         w64_mfma_drain();   // the last PV MFMAs have written O
 #pragma unroll
