@@ -43,7 +43,8 @@ def _run(cmd: list[str], cwd: Path = ROOT) -> None:
         raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{err}")
 
 
-CAPI_SOURCES = ("attn_capi.hip", "softmax_capi.hip")
+CAPI_SOURCES = ("attn_capi.hip", "softmax_capi.hip", "attn_fwd_w64_bf16_causal.hip", "attn_fwd_w64_bf16_full.hip",
+                "attn_fwd_w64_f16_causal.hip", "attn_fwd_w64_f16_full.hip")
 
 
 def build_capi() -> Path:

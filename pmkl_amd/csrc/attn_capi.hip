@@ -25,6 +25,22 @@
 #include "attn_bwd_kernels.hpp"
 #include "attn_bwd_f32.hpp"
 
+// The 64-row forward kernels are instantiated in attn_fwd_w64_<dtype>_<mask>.hip
+// (one translation unit each, compiled in parallel).
+namespace pmkl_amd {
+#define PMKL_W64_EXTERN(T, C)                                                            \
+    extern template __global__ void attn_fwd_w64_kernel<T, 64, C, 1, 8>(AttnParams);  \
+    extern template __global__ void attn_fwd_w64_kernel<T, 128, C, 1, 8>(AttnParams); \
+    extern template __global__ void attn_fwd_w64_kernel<T, 32, C, 2, 4>(AttnParams);  \
+    extern template __global__ void attn_fwd_w64_kernel<T, 64, C, 2, 4>(AttnParams);  \
+    extern template __global__ void attn_fwd_w64_kernel<T, 128, C, 2, 4>(AttnParams);
+PMKL_W64_EXTERN(__bf16, true)
+PMKL_W64_EXTERN(__bf16, false)
+PMKL_W64_EXTERN(_Float16, true)
+PMKL_W64_EXTERN(_Float16, false)
+#undef PMKL_W64_EXTERN
+}  // namespace pmkl_amd
+
 namespace {
 
 using pmkl_capi::dtype_size;

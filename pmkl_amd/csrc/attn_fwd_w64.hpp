@@ -57,8 +57,10 @@ namespace pmkl_amd {
 // One LDS-DMA of 16 bytes per lane: bytes [off, off+16) of buffer r land at
 // LDS byte address m0 + 16 * lane.  Inline asm, so the compiler neither waits
 // for it before unrelated LDS reads nor counts it; the kernel waits itself.
+// An SALU write of M0 needs one wait state before an LDS-DMA reads it.
 __device__ __forceinline__ void w64_lds_dma16(__amdgpu_buffer_rsrc_t r, int off, unsigned m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0), "s"(r)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0),
+                 "s"(r)
                  : "memory");
 }
 

@@ -1,0 +1,14 @@
+// Explicit instantiations of the 64-row forward kernel for _Float16, non-causal:
+// compiled as a translation unit of its own so that the library's kernels
+// build in parallel (attn_capi.hip declares them extern).
+#include <hip/hip_runtime.h>
+
+#include "attn_fwd_w64.hpp"
+
+namespace pmkl_amd {
+template __global__ void attn_fwd_w64_kernel<_Float16, 64, false, 1, 8>(AttnParams);
+template __global__ void attn_fwd_w64_kernel<_Float16, 128, false, 1, 8>(AttnParams);
+template __global__ void attn_fwd_w64_kernel<_Float16, 32, false, 2, 4>(AttnParams);
+template __global__ void attn_fwd_w64_kernel<_Float16, 64, false, 2, 4>(AttnParams);
+template __global__ void attn_fwd_w64_kernel<_Float16, 128, false, 2, 4>(AttnParams);
+}  // namespace pmkl_amd
