@@ -222,8 +222,9 @@ template <int D, int QB> struct W64Sched {
     static constexpr int MS0 = QKS + 2;
     static constexpr int max_slot(int k) { return MS0 + k * (NSLOT - 1 - MS0) / (NMU - 1); }
 
-    // DMAs of the iteration, all before the barrier.
-    static constexpr int dma_slot(int j, int n) { return 1 + j * (BARS - 1) / n; }
+    // DMAs of the iteration, in the n slots right before the barrier (measured
+    // ~1% faster than spreading them over the slots before it).
+    static constexpr int dma_slot(int j, int n) { return BARS - n + j; }
 
     static constexpr bool valid() {
         for (int n = 0; n < NU; ++n)
@@ -259,6 +260,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     constexpr int CPR = D / 8;              // 16-byte chunks per row
     constexpr int TILE_CHUNKS = BN * CPR;   // chunks per K (or V) tile
     constexpr int LOADS = TILE_CHUNKS / NT;   // DMAs per thread per tensor per tile
+    static_assert(Sch::BARS >= 2 * LOADS, "the DMAs of an iteration issue before its barrier");
     constexpr int TILE_BYTES = BN * D * (int)sizeof(T);
     constexpr int NDB = Sch::NDB, NDK = Sch::NDK, NKF = Sch::NKF, NF = Sch::NF;
     constexpr int NSLOT = Sch::NSLOT, RING = Sch::RING;
