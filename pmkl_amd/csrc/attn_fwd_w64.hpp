@@ -41,13 +41,16 @@
 // first VALU access of an MFMA result, and P written a full slot before the
 // MFMA that reads it).
 //
-// LDS: K/V tiles reach LDS by LDS-DMA (buffer_load ... lds) into three slots
-// each, K(t) and V(t) in slot t % 3.  Iteration t issues the DMAs of K(t+3)
-// and V(t+2); one barrier per iteration, BARS slots in, after the wave's last
-// LDS read of K(t+1) and V(t), preceded by a wait for the DMAs of iteration
-// t-1 (K(t+2), V(t+1)).  So a DMA only overwrites a slot all waves have
-// finished reading (K(t), V(t-1), read before the previous barrier), and a
-// tile is read only after the barrier that follows its arrival.
+// LDS: K/V tiles reach LDS by LDS-DMA (buffer_load ... lds) into four slots
+// each, K(t) and V(t) in slot t % 4; an item's stream positions are rounded
+// up to a multiple of four, so every item starts in slot 0 and the unrolled
+// loop addresses the slots at compile time.  Iteration t issues the DMAs of
+// K(t+3) and V(t+2) in the slots right before its barrier (BARS), which
+// follows the wave's last LDS read of K(t+1) and V(t) and a wait for the
+// DMAs of iteration t-1 (K(t+2), V(t+1)).  So a DMA only overwrites a slot
+// all waves have finished reading (K(t-1), V(t-2), read before the previous
+// barrier), and a tile is read only after the barrier that follows its
+// arrival.
 #pragma once
 
 #include "attn_fwd_kernels.hpp"
