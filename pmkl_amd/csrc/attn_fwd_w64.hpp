@@ -311,7 +311,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     // Next item: its first tiles are loaded during the current item's last
     // iterations.
     bool has_next = false;
-    int nt_n = 1;
+    int nt_n = 1, bh_nx = 0, q0w_nx = 0;   // next item: tiles, head, first row of the wave
     const T *kg_n = nullptr, *vg_n = nullptr;
     auto head_ptrs = [&](int bh_, const T *&kp, const T *&vp) __attribute__((always_inline)) {
         const int b_ = bh_ / p.H, h_ = bh_ - b_ * p.H;
@@ -337,22 +337,23 @@ void attn_fwd_w64_kernel(AttnParams p) {
     auto set_next = [&](int L) __attribute__((always_inline)) {
         has_next = L < n_items;
         if (has_next) {
-            int bh_n, qt_n;
-            map_index<CAUSAL>(p, L, bh_n, qt_n);
+            int qt_n;
+            map_index<CAUSAL>(p, L, bh_nx, qt_n);
             nt_n = item_tiles(qt_n);
-            head_ptrs(bh_n, kg_n, vg_n);
+            q0w_nx = qt_n * kBlockM + wave_row;
+            head_ptrs(bh_nx, kg_n, vg_n);
         }
     };
 
     // Q fragments of the current item (B operand of S^T = K Q^T, AGPRs):
     // block qb, lane holds Q[q0w + 32 qb + col][16 dk + 8 hi .. +7].
     frag qf[QB][NDK];
-    auto load_q = [&]() __attribute__((always_inline)) {
-        const int b_ = bh / p.H, h_ = bh - b_ * p.H;
+    auto load_q_of = [&](int bh_q, int q0w_q) __attribute__((always_inline)) {
+        const int b_ = bh_q / p.H, h_ = bh_q - b_ * p.H;
         const T *qg = (const T *)p.q + b_ * p.q_sb + h_ * p.q_sh;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            const int qrow = min(q0w + 32 * qb + col, S - 1);
+            const int qrow = min(q0w_q + 32 * qb + col, S - 1);
             const T *src = qg + (int64_t)qrow * p.q_ss + 8 * hi;
 #pragma unroll
             for (int dk = 0; dk < NDK; ++dk)
@@ -363,6 +364,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     // allocator may keep them in VGPRs and copy before each use).  The pin
     // waits for the loads, so it sits after the previous item's O stores:
     // the load latency overlaps them.
+    auto load_q = [&]() __attribute__((always_inline)) { load_q_of(bh, q0w); };
     auto pin_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
@@ -773,7 +775,10 @@ void attn_fwd_w64_kernel(AttnParams p) {
             for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
             apply_rescale();
         }
-        sync_tiles();   // every wave is done with K(0) before its slot is refilled
+        // No barrier here: iteration 0 refills slots 3 and 2 (K(3), V(2)),
+        // free since the previous item's last barrier, and K(0), V(0), K(1)
+        // landed before it.  (So the epilogue's O stores are not waited for
+        // until iteration 0's barrier.)
         {
             const uint32_t k1 = k_slot_base(1);
 #pragma unroll
@@ -793,6 +798,10 @@ void attn_fwd_w64_kernel(AttnParams p) {
             iteration(t, std::integral_constant<int, 3>{});
             ++t;
         }
+        // A wave with DMA-only positions left no longer reads Q: the next
+        // item's Q loads go out now and land under those positions.
+        const bool q_early = has_next && t < npos;
+        if (q_early) load_q_of(bh_nx, q0w_nx);
         // ---- remaining positions of the item: DMAs and barriers only ----
         for (; t < npos; ++t) {
 #pragma unroll
@@ -811,7 +820,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
             ++r;
             set_item(item_index(r));
             set_next(item_index(r + 1));
-            load_q();
+            if (!q_early) load_q();
         }
         store_item(bh_e, q0w_e, active_e);
         if (!more) break;
