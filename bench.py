@@ -39,16 +39,19 @@ METRIC = "causal-attn TFLOP/s on 1 MI355X, bf16 B4 H32 S4096 D128; % of MFMA pea
 
 
 def kernel_name(w) -> str:
-    """Kernel the C ABI dispatches for workload w (its dispatch rule, restated
-    for the bench line's label): fp32 -> the fp32 kernel; 16-bit -> the
-    64-row kernel for head_dim 128 and S > 128 unless PMKL_ATTN_W64=0
-    (=1 also takes it at head_dim 32 and 64), else the 4- or 8-wave MFMA
-    kernel."""
+    """Kernel the C ABI dispatches for the causal workload w (its dispatch
+    rule, restated for the bench line's label): fp32 -> the fp32 kernel;
+    16-bit -> the 64-row kernel for S > 128 at head_dim 128, and at head_dim
+    64 from S = 512 on, unless PMKL_ATTN_W64=0 (=1 takes it at every head_dim
+    for S > 128), else the 4- or 8-wave MFMA kernel."""
     if w.dtype == "fp32":
         return "attn_fwd_f32_kernel"
     mode = os.environ.get("PMKL_ATTN_W64")
-    w64 = (mode == "1" or (mode is None and w.D >= 128)) and w.S > 128
-    return "attn_fwd_w64_kernel" if w64 else "attn_fwd_mfma16_kernel"
+    if mode is None:
+        w64 = w.D >= 128 or (w.D == 64 and w.S >= 512)
+    else:
+        w64 = mode == "1"
+    return "attn_fwd_w64_kernel" if w64 and w.S > 128 else "attn_fwd_mfma16_kernel"
 WARMUP_MIN_S = 1.0
 
 

@@ -75,11 +75,25 @@ int waves16(int64_t D, int64_t S, bool causal) {
     return (causal && D == 64 && S > 512 && S <= 2048) ? 4 : 8;
 }
 
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, int NTR = 0>
 KernelChoice pick16w(bool causal) {
-    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, true, NW>
-                   : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW>,
+    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, true, NW, NTR>
+                   : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW, NTR>,
             NW * 64, NW * 32};
+}
+// Key tiles (of 64) the resident form of the 8-wave kernel holds in LDS:
+// NTR * 2 * 64 * D * 2 bytes, 32 KiB at head_dim 32, 64 KiB at 64 and 128.
+constexpr int resident_tiles(int64_t D) { return D == 128 ? 2 : 4; }
+
+// Resident form (all key tiles loaded at once, no barrier per tile) for
+// sequences of at most resident_tiles(D) key tiles, unless
+// PMKL_ATTN_RESIDENT=0 (read once).
+bool resident_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("PMKL_ATTN_RESIDENT");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
 }
 // 64-row kernel choice: PMKL_ATTN_W64=0 never, =1 wherever it applies,
 // unset: for head_dim 128, and for causal head_dim 64 from S = 512 on (in its
@@ -138,11 +152,12 @@ KernelChoice pick_w32(int64_t D, bool causal) {
 }
 
 template <typename T, int D>
-KernelChoice pick16(bool causal, bool w64, int waves) {
+KernelChoice pick16(bool causal, bool w64, int waves, bool resident) {
     if (w64)
         return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, true>
                        : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false>,
                 256, 256};
+    if (resident) return pick16w<T, D, 8, resident_tiles(D)>(causal);
     return waves == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
 }
 template <int D>
@@ -152,17 +167,17 @@ KernelChoice pick32(bool causal) {
             pmkl_amd::kThreads, pmkl_amd::kBlockM};
 }
 
-KernelChoice select_kernel(int32_t dt, int64_t d, bool causal, bool w64, int waves) {
+KernelChoice select_kernel(int32_t dt, int64_t d, bool causal, bool w64, int waves, bool resident) {
     switch (dt) {
         case PMKL_DTYPE_BF16:
-            if (d == 32) return pick16<__bf16, 32>(causal, w64, waves);
-            if (d == 64) return pick16<__bf16, 64>(causal, w64, waves);
-            if (d == 128) return pick16<__bf16, 128>(causal, w64, waves);
+            if (d == 32) return pick16<__bf16, 32>(causal, w64, waves, resident);
+            if (d == 64) return pick16<__bf16, 64>(causal, w64, waves, resident);
+            if (d == 128) return pick16<__bf16, 128>(causal, w64, waves, resident);
             break;
         case PMKL_DTYPE_F16:
-            if (d == 32) return pick16<_Float16, 32>(causal, w64, waves);
-            if (d == 64) return pick16<_Float16, 64>(causal, w64, waves);
-            if (d == 128) return pick16<_Float16, 128>(causal, w64, waves);
+            if (d == 32) return pick16<_Float16, 32>(causal, w64, waves, resident);
+            if (d == 64) return pick16<_Float16, 64>(causal, w64, waves, resident);
+            if (d == 128) return pick16<_Float16, 128>(causal, w64, waves, resident);
             break;
         case PMKL_DTYPE_F32:
             if (d == 32) return pick32<32>(causal);
@@ -460,8 +475,11 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
                      a->dtype != PMKL_DTYPE_F32 && S > 128 && head_span_ok(ks) && head_span_ok(vs);
     const bool w32 = w64 && (D == 64 || D == 128) && w32_mode() == 1;
     const bool bf = a->dtype == PMKL_DTYPE_BF16;
+    const int waves = waves16(D, S, causal);
+    const bool resident = !w64 && a->dtype != PMKL_DTYPE_F32 && waves == 8 &&
+                          (S + 63) / 64 <= resident_tiles(D) && resident_enabled();
     const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(D, causal) : pick_w32<_Float16>(D, causal))
-                                : select_kernel(a->dtype, D, causal, w64, waves16(D, S, causal));
+                                : select_kernel(a->dtype, D, causal, w64, waves, resident);
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
     const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;

@@ -87,6 +87,15 @@ __device__ __forceinline__ float half_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
 // Row of the K tile fed to MFMA A-row i (0..31) of a 32-key block.  A-row
 // i = 8g + 4h + t lands in accumulator register 4g + t of lane half h, so
 // feeding it key 16h + 4g + t gives lane half h the keys 16h .. 16h+15 in
@@ -181,8 +190,15 @@ __device__ __forceinline__ void map_workgroup(const AttnParams &p, int &bh, int 
 
 // ---------------------------------------------------------------------------
 // 16-bit kernel (bf16 / fp16), head_dim D in {32, 64, 128}
+//
+// NTR = 0: K/V tiles stream through a two-stage LDS ring, one barrier per
+// tile.  NTR > 0 (short sequences, host guarantees ceil(S / 64) <= NTR): the
+// loads of every key tile of the workgroup are issued at once, each tile gets
+// its own LDS stage, and after one barrier the waves run their tiles with no
+// further barrier, so a work item waits for memory once instead of once per
+// tile.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL, int NW>
+template <typename T, int D, bool CAUSAL, int NW, int NTR = 0>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnParams p) {
     using E = Elt16<T>;
     using frag = typename E::frag;
@@ -195,8 +211,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     constexpr bool PARTIAL = TILE_CHUNKS % kThreads != 0;   // some threads idle in the last load
     constexpr int NDB = D / 32;             // 32-wide blocks of head_dim
     constexpr int NDK = D / 16;             // 16-deep MFMA steps over head_dim
+    constexpr int NST = NTR > 0 ? NTR : 2;  // LDS stages (and register sets)
 
-    __shared__ __attribute__((aligned(16))) T smem[2][2][BN * D];  // [stage][K,V]
+    __shared__ __attribute__((aligned(16))) T smem[NST][2][BN * D];  // [stage][K,V]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -241,9 +258,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     // at its first key and ends at the last key of the sequence, so rows past
     // the end read as zero (those keys are masked) and the per-thread byte
     // offsets are the same for every tile.
-    // Two register sets: the loads of tile t go to set t & 1 two tiles ahead
-    // of use, so a load has two steps to land before its LDS write.
-    u32x4_t kreg[2][LOADS], vreg[2][LOADS];
+    // Streaming: two register sets; the loads of tile t go to set t & 1 two
+    // tiles ahead of use, so a load has two steps to land before its LDS
+    // write.  Resident: one set per tile.
+    u32x4_t kreg[NST][LOADS], vreg[NST][LOADS];
     int koff[LOADS], voff[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
@@ -306,26 +324,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     const int vrow0 = 16 * (g >> 1) + (tt >> 2);
     const int vcol0 = 16 * (g & 1) + 4 * (tt & 3);
 
-    gload(0, std::integral_constant<int, 0>{});
-    swrite(0, std::integral_constant<int, 0>{});
-    // Q fragments and tile 0 have landed before the loop, so no vmcnt wait is
-    // needed before the score MFMAs of a tile; tile 1 is left in flight.
-    __builtin_amdgcn_s_waitcnt(0);
-    gload(min(1, nt - 1), std::integral_constant<int, 1>{});
-    __syncthreads();
-
-    // Tile kt: LDS stage kt & 1; its registers (set kt & 1) are refilled with
-    // tile kt + 2, and tile kt + 1 (set (kt+1) & 1) goes to the other stage.
-    auto tile_step = [&](auto set_c, int kt) {
-        constexpr int SET = decltype(set_c)::value;
-        constexpr int st = SET;
-        // Issued on every step (a clamped tile near the end) so that the
-        // number of loads in flight, and hence the vmcnt wait before the LDS
-        // write below, is the same on every path.
-        gload(min(kt + 2, nt - 1), set_c);
+    // One key tile kt of this wave from LDS stage st: scores, mask, online
+    // softmax, O update.
+    auto compute_tile = [&](int st, int kt) __attribute__((always_inline)) {
         const int kbase = kt * BN;
-        const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
-        if (wave_needed) {
+        {
             const T *Ks = smem[st][0];
             const T *Vs = smem[st][1];
             // ---- S^T = K Q^T for two 32-key blocks ----
@@ -412,12 +415,49 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                     }
                 }
         }
-        if (kt + 1 < nt) swrite(st ^ 1, std::integral_constant<int, SET ^ 1>{});
-        __syncthreads();
     };
-    for (int kt = 0; kt < nt; kt += 2) {
-        tile_step(std::integral_constant<int, 0>{}, kt);
-        if (kt + 1 < nt) tile_step(std::integral_constant<int, 1>{}, kt + 1);
+    auto wave_needs = [&](int kt) __attribute__((always_inline)) { return wave_active && (!CAUSAL || kt * BN <= q0w + 31); };
+
+    if constexpr (NTR > 0) {
+        // All key tiles of the workgroup at once (nt <= NTR): issue every
+        // load, wait once, write each tile to its own stage, one barrier.
+        static_for<NTR>([&](auto t_c) {
+            constexpr int t = decltype(t_c)::value;
+            if (t < nt) gload(t, t_c);
+        });
+        __builtin_amdgcn_s_waitcnt(0);
+        static_for<NTR>([&](auto t_c) {
+            constexpr int t = decltype(t_c)::value;
+            if (t < nt) swrite(t, t_c);
+        });
+        __syncthreads();
+        // No barrier from here on: each wave runs its own tiles and leaves.
+        for (int kt = 0; kt < nt && wave_needs(kt); ++kt) compute_tile(kt, kt);
+    } else {
+        gload(0, std::integral_constant<int, 0>{});
+        swrite(0, std::integral_constant<int, 0>{});
+        // Q fragments and tile 0 have landed before the loop, so no vmcnt wait is
+        // needed before the score MFMAs of a tile; tile 1 is left in flight.
+        __builtin_amdgcn_s_waitcnt(0);
+        gload(min(1, nt - 1), std::integral_constant<int, 1>{});
+        __syncthreads();
+
+        // Tile kt: LDS stage kt & 1; its registers (set kt & 1) are refilled with
+        // tile kt + 2, and tile kt + 1 (set (kt+1) & 1) goes to the other stage.
+        auto tile_step = [&](auto set_c, int kt) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+            // Issued on every step (a clamped tile near the end) so that the
+            // number of loads in flight, and hence the vmcnt wait before the LDS
+            // write below, is the same on every path.
+            gload(min(kt + 2, nt - 1), set_c);
+            if (wave_needs(kt)) compute_tile(SET, kt);
+            if (kt + 1 < nt) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
+            __syncthreads();
+        };
+        for (int kt = 0; kt < nt; kt += 2) {
+            tile_step(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < nt) tile_step(std::integral_constant<int, 1>{}, kt + 1);
+        }
     }
 
     // ---- epilogue: normalise, store O, m, l ----
