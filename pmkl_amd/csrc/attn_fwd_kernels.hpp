@@ -236,7 +236,22 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     T *og = (T *)p.o + b * p.o_sb + h * p.o_sh;
 
     const int q0 = qt * kBlockM;
-    const int q0w = q0 + 32 * wave;
+    // 32-row block of this wave.  Resident form (one query tile; nb blocks
+    // hold rows, block b needs b / 2 + 1 key tiles): waves w and w + 4 share
+    // a SIMD, and with no barrier between tiles the SIMD with the most tiles
+    // sets the time.  With P = nb - 4 SIMDs that must take two blocks, the
+    // 2P shortest blocks are paired short with long (0 with 2P - 1, 1 with
+    // 2P - 2, ...) and the longest ones run alone: at S = 256, 5 tiles per
+    // SIMD instead of up to 6.
+    int rb = wave;
+    if constexpr (NTR > 0 && CAUSAL && NW == 8) {
+        const int P = max(0, min(8, (S + 31) >> 5) - 4);
+        if (wave < 4)
+            rb = wave < P ? wave : P + wave;
+        else if (wave - 4 < P)
+            rb = 2 * P - 1 - (wave - 4);
+    }
+    const int q0w = q0 + 32 * rb;
     const int qi = q0w + col;                         // this lane's query row
     const int last_key = CAUSAL ? min(q0 + kBlockM - 1, S - 1) : S - 1;
     const int nt = last_key / BN + 1;                 // key tiles for the workgroup
@@ -352,12 +367,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             if (need_mask) {
                 const int lim = CAUSAL ? min(qi, S - 1) : S - 1;   // last visible key
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 2; ++kb) {
+                    // register r holds key kbase + 32kb + 16hi + r: visible iff r <= d
+                    const int d = lim - (kbase + 32 * kb + 16 * hi);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = kbase + 32 * kb + 16 * hi + r;
-                        if (key > lim) sacc[kb][r] = -INFINITY;
-                    }
+                    for (int r = 0; r < 16; ++r)
+                        if (r > d) sacc[kb][r] = -INFINITY;
+                }
             }
             // ---- online softmax ----
             float mx = sacc[0][0];

@@ -122,10 +122,13 @@ __device__ __forceinline__ void w64_fence_v(f32x16_t &x) { asm volatile("" : "+v
 
 // s = (R <= d) ? s : -inf, through VCC: left to itself the compiler computes
 // all compares of a tile into separate SGPR pairs first, and that pressure
-// spills long-lived SGPRs for the whole loop.
+// spills long-lived SGPRs for the whole loop.  A VALU write of VCC needs two
+// wait states before v_cndmask reads it as the lane mask (the compiler keeps
+// the same distance in its own code for gfx950), hence the s_nop 1.
 template <int R>
 __device__ __forceinline__ float w64_mask_key(float s, int d) {
-    asm volatile("v_cmp_le_i32 vcc, %1, %2\n\tv_cndmask_b32 %0, %3, %0, vcc" : "+v"(s) : "n"(R), "v"(d), "v"(-INFINITY) : "vcc");
+    asm volatile("v_cmp_le_i32 vcc, %1, %2\n\ts_nop 1\n\tv_cndmask_b32 %0, %3, %0, vcc"
+                 : "+v"(s) : "n"(R), "v"(d), "v"(-INFINITY) : "vcc");
     return s;
 }
 // Row-max steps as single instructions: fmaxf on MFMA results (opaque to the
