@@ -41,6 +41,8 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
 // Kernel parameters.  Strides are in elements; head_dim is contiguous.
 struct AttnParams {
@@ -120,6 +122,13 @@ template <> struct Elt16<__bf16> {
         const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
         return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, packed), one, acc, false);
     }
+    // c + the lane's own four packed values, in every register of c: 16
+    // blocks of 4x4x4 with an all-ones A operand (lane 4i + j of block i
+    // holds column j of B and receives column j of the product).
+    static __device__ __forceinline__ f32x4_t sum4(u32x2_t packed, f32x4_t c) {
+        const s16x4_t one = {0x3f80, 0x3f80, 0x3f80, 0x3f80};   // bf16 1.0
+        return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(one, __builtin_bit_cast(s16x4_t, packed), c, 0, 0, 0);
+    }
 };
 template <> struct Elt16<_Float16> {
     typedef f16x8_t frag;
@@ -133,6 +142,10 @@ template <> struct Elt16<_Float16> {
     static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
         const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
         return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, packed), one, acc, false);
+    }
+    static __device__ __forceinline__ f32x4_t sum4(u32x2_t packed, f32x4_t c) {
+        const f16x4_t one = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_mfma_f32_4x4x4f16(one, __builtin_bit_cast(f16x4_t, packed), c, 0, 0, 0);
     }
 };
 
@@ -330,7 +343,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     // with their usual relative precision.
     float m_true = -INFINITY;
     float m_use = -INFINITY;
-    float l_run = 0.f;         // per-lane partial row sum relative to m_use
+    // Per-lane partial row sums relative to m_use, accumulated by 4x4x4
+    // MFMAs (sum4) into component 0 .. 3 alike; two accumulators alternate so
+    // that consecutive row-sum MFMAs do not wait on each other.
+    f32x4_t lsum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     const float lazy_raw = kLazyLog2 / p.scale_log2;
 
     // Per-lane constant parts of the LDS addresses.
@@ -389,7 +405,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                 const float m_new = fmaxf(m_use, mx);
                 const float alpha = fast_exp2((m_use - m_new) * p.scale_log2);  // 0 on the first tile
                 m_use = m_new;
-                l_run *= alpha;
+                lsum[0] *= alpha;
+                lsum[1] *= alpha;
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -404,9 +421,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                     const float p0 = fast_exp2(__builtin_fmaf(sacc[kb][r], p.scale_log2, moff));
                     const float p1 = fast_exp2(__builtin_fmaf(sacc[kb][r + 1], p.scale_log2, moff));
                     pk[kb][r >> 1] = E::pack2(p0, p1);
-                    // l sums the probabilities as rounded for the PV product, so
-                    // O is normalised by exactly the weights it was built from.
-                    l_run = E::sum2(pk[kb][r >> 1], l_run);
+                }
+            // l sums the probabilities as rounded for the PV product, so O is
+            // normalised by exactly the weights it was built from.
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const u32x2_t pair = {pk[kb][2 * c], pk[kb][2 * c + 1]};
+                    lsum[c & 1] = E::sum4(pair, lsum[c & 1]);
                 }
             // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -477,7 +500,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     }
 
     // ---- epilogue: normalise, store O, m, l ----
-    const float l_sum = half_sum(l_run);   // relative to m_use
+    const float l_sum = half_sum(lsum[0][0] + lsum[1][0]);   // relative to m_use
     if (wave_active && qi < S) {
         const float inv = 1.0f / l_sum;
         // l of the output is relative to the exact row max
