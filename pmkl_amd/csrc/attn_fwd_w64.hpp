@@ -752,10 +752,15 @@ void attn_fwd_w64_kernel(AttnParams p) {
     }
     sync_tiles();
 
+    // Outputs of the previous item (its O, row sums and maxima stay in acc,
+    // lsum, m_true, m_use until written): stored under the next item's first
+    // score MFMAs, after the wait for that item's Q, so neither the stores
+    // nor their normalisation hold up the item start.
+    bool have_prev = false, active_p = false;
+    int bh_p = 0, q0w_p = 0;
     while (true) {
         pin_q();
         // Scores and maxima of tile 0 (slot 0; landed, see above).
-        reset_state();
         {
             const uint32_t k0 = k_slot_base(0);
 #pragma unroll
@@ -768,6 +773,10 @@ void attn_fwd_w64_kernel(AttnParams p) {
                     else M::qk(sc[0][qb][kb], a, qf[qb][dk]);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+            if (have_prev) store_item(bh_p, q0w_p, active_p);
+            reset_state();
+            __builtin_amdgcn_sched_barrier(0);
             w64_mfma_drain();
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb)
@@ -815,8 +824,9 @@ void attn_fwd_w64_kernel(AttnParams p) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) fence_block(qb);
 
-        // Next item first (its Q loads overlap this item's epilogue), then
-        // this item's outputs.
+        // Next item (its Q loads land under the DMA-only positions or the
+        // next loop head); this item's outputs go out there, or now after the
+        // last item.
         const int bh_e = bh, q0w_e = q0w;
         const bool active_e = wave_active, more = has_next;
         if (more) {
@@ -825,8 +835,14 @@ void attn_fwd_w64_kernel(AttnParams p) {
             set_next(item_index(r + 1));
             if (!q_early) load_q();
         }
-        store_item(bh_e, q0w_e, active_e);
-        if (!more) break;
+        if (!more) {
+            store_item(bh_e, q0w_e, active_e);
+            break;
+        }
+        have_prev = true;
+        bh_p = bh_e;
+        q0w_p = q0w_e;
+        active_p = active_e;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // no DMA outlives the workgroup
 }
