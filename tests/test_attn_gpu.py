@@ -173,6 +173,32 @@ def test_many_items_per_workgroup(device, B, H, S, D, dtype, causal):
     _say(f"{tag}: {errs}")
 
 
+# (D, S): every sequence length class of the resident 8-wave form (all key
+# tiles in LDS at once): 5 to 8 row blocks of 32 (the SIMD pairing of short
+# and long blocks changes with each), ragged last blocks and tiles, and the
+# head_dim-128 limit of two key tiles.
+RESIDENT_SHAPES = [(32, 160), (32, 193), (32, 224), (32, 255), (64, 192), (64, 225), (64, 256),
+                   (128, 65), (128, 127), (128, 128)]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_resident_short_sequences(device, dtype, causal):
+    """Short sequences (S <= 256, S <= 128 at head_dim 128) run the 8-wave
+    kernel with every key tile resident in LDS and SIMD-balanced row blocks:
+    all rows against the oracle."""
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+
+    for i, (D, S) in enumerate(RESIDENT_SHAPES):
+        B, H = 2, 3
+        tag = f"{dtype} B{B} H{H} S{S} D{D} causal={causal} (resident)"
+        _say(f"case {tag}")
+        q, k, v = small_inputs(B, H, S, D, dtype, seed=7300 + 10 * i)
+        o, m, l = _run_capi(q, k, v, device, causal=causal)
+        check_outputs(q, k, v, o, m, l, dtype, causal=causal, label=tag)
+
+
 @pytest.mark.parametrize("S", [513, 1000, 2048])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 @pytest.mark.parametrize("causal", [True, False])
