@@ -39,6 +39,8 @@ PMKL_W64_EXTERN(__bf16, false)
 PMKL_W64_EXTERN(_Float16, true)
 PMKL_W64_EXTERN(_Float16, false)
 #undef PMKL_W64_EXTERN
+extern template __global__ void attn_fwd_w64_kernel<__bf16, 64, true, 1, 4>(AttnParams);
+extern template __global__ void attn_fwd_w64_kernel<_Float16, 64, true, 1, 4>(AttnParams);
 }  // namespace pmkl_amd
 
 namespace {
@@ -56,6 +58,7 @@ struct KernelChoice {
     kernel_fn fn;
     int threads;
     int block_m;
+    int per_cu = 1;   // persistent workgroups per CU (64-row kernel)
 };
 
 // PMKL_ATTN_WAVES=4 or 8 pins the waves of the 16-bit MFMA kernel; 0 if unset.
@@ -146,8 +149,23 @@ KernelChoice pick_w32(bool causal) {
                    : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false, 1, 8>,
             512, 256};
 }
+// Two 128-row workgroups per CU for small causal head_dim-64 problems unless
+// PMKL_ATTN_SPLIT=0 (read once).
+bool split_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("PMKL_ATTN_SPLIT");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
+// split: causal head_dim 64 with fewer 256-row work items than two per CU
+// runs two 128-row workgroups per CU instead (measured same-box: B1 H8 S8192
+// 129 -> 102 us, B3 H5 S700 16.4 -> 13.0 us; equal at C2, 1-2% slower with
+// two or more 256-row items per CU).
 template <typename T>
-KernelChoice pick_w32(int64_t D, bool causal) {
+KernelChoice pick_w32(int64_t D, bool causal, bool split) {
+    if (D == 64 && causal && split) return {(kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 64, true, 1, 4>, 256, 128, 2};
     return D == 64 ? pick_w32<T, 64>(causal) : pick_w32<T, 128>(causal);
 }
 
@@ -478,7 +496,9 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     const int waves = waves16(D, S, causal);
     const bool resident = !w64 && a->dtype != PMKL_DTYPE_F32 && waves == 8 &&
                           (S + 63) / 64 <= resident_tiles(D) && resident_enabled();
-    const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(D, causal) : pick_w32<_Float16>(D, causal))
+    const bool split = w32 && D == 64 && causal && split_enabled() &&
+                       B * H * ((S + 255) / 256) < 2 * (int64_t)cu_count();
+    const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(D, causal, split) : pick_w32<_Float16>(D, causal, split))
                                 : select_kernel(a->dtype, D, causal, w64, waves, resident);
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
@@ -519,7 +539,7 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     if (w64) {
         const int cus = cu_count();
         PMKL_REQUIRE(cus > 0, PMKL_EHIP, "could not read the device's CU count");
-        grid = std::min<int64_t>(grid, cus);
+        grid = std::min<int64_t>(grid, (int64_t)kc.per_cu * cus);
     }
     hipLaunchKernelGGL(kc.fn, dim3((unsigned)grid), dim3(kc.threads), 0, st, p);
     hipError_t err = hipGetLastError();

@@ -248,12 +248,15 @@ template <int D, int QB> struct W64Sched {
     static_assert(valid(), "slot schedule");
 };
 
-// QB 32-row query blocks per wave, NW waves per workgroup (NW / 4 per SIMD),
-// 32 QB NW = 256 query rows per workgroup: (QB, NW) = (2, 4) is one wave of 64
-// rows per SIMD; (1, 8) two waves of 32 rows per SIMD, each running the same
-// slot schedule, so that one wave issues while the other waits.
+// QB 32-row query blocks per wave, NW waves per workgroup, 32 QB NW query
+// rows per workgroup: (QB, NW) = (2, 4) is one wave of 64 rows per SIMD;
+// (1, 8) two waves of 32 rows per SIMD, each running the same slot schedule,
+// so that one wave issues while the other waits; (1, 4) the same two waves
+// per SIMD from two workgroups of 128 rows on one CU (head_dim 64: 64 KiB of
+// LDS each), which halves the work item for problems with few items.
 template <typename T, int D, bool CAUSAL, int QB = 2, int NW = 4>
-__global__ __launch_bounds__(64 * NW, 1) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+__global__ __launch_bounds__(64 * NW, (QB == 1 && NW == 4) ? 2 : 1)
+__attribute__((amdgpu_waves_per_eu(QB == 1 ? 2 : NW / 4, QB == 1 ? 2 : NW / 4)))
 void attn_fwd_w64_kernel(AttnParams p) {
     using E = Elt16<T>;
     using M = W64Mma<T>;
@@ -261,7 +264,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     using frag = typename E::frag;
     constexpr int NT = 64 * NW;             // threads per workgroup
     constexpr int kBlockM = 32 * QB * NW;   // query rows per workgroup
-    static_assert(kBlockM == 256, "work items are 256-row query tiles");
+    static_assert(kBlockM == 256 || (kBlockM == 128 && QB == 1), "work items are 256- or 128-row query tiles");
     constexpr int BN = 64;                  // keys per tile
     constexpr int CPR = D / 8;              // 16-byte chunks per row
     constexpr int TILE_CHUNKS = BN * CPR;   // chunks per K (or V) tile

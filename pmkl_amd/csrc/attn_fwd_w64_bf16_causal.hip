@@ -7,6 +7,7 @@
 
 namespace pmkl_amd {
 template __global__ void attn_fwd_w64_kernel<__bf16, 64, true, 1, 8>(AttnParams);
+template __global__ void attn_fwd_w64_kernel<__bf16, 64, true, 1, 4>(AttnParams);
 template __global__ void attn_fwd_w64_kernel<__bf16, 128, true, 1, 8>(AttnParams);
 template __global__ void attn_fwd_w64_kernel<__bf16, 32, true, 2, 4>(AttnParams);
 template __global__ void attn_fwd_w64_kernel<__bf16, 64, true, 2, 4>(AttnParams);
