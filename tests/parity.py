@@ -39,9 +39,12 @@ def to_np(t):
     return t.detach().to("cpu", torch.float32).numpy().astype(np.float64)
 
 
-def check_outputs(q, k, v, o, m, l, dtype: str, causal: bool = True, rows=None, scale=None, label=""):
+def check_outputs(q, k, v, o, m, l, dtype: str, causal: bool = True, rows=None, scale=None, label="",
+                  check_ml: bool = True):
     """q, k, v: CPU torch tensors [B, H, S, D] (in `dtype`); o, m, l: device or
     CPU outputs.  rows: None (all rows) or the row indices to compare.
+    check_ml=False reports m and l but asserts only O (for callers that hold
+    m and l to a bound of their own).
     Returns a dict of the errors; raises AssertionError beyond tolerance."""
     B, H, S, D = q.shape
     qn, kn, vn = (to_np(x).reshape(B * H, S, D) for x in (q, k, v))
@@ -79,6 +82,8 @@ def check_outputs(q, k, v, o, m, l, dtype: str, causal: bool = True, rows=None, 
     _log(label, dtype, (B, H, S, D), causal, rows, report)
     assert worst <= 1.0, (f"{label}: O beyond bound: max|dO| {err_o:.3g} (tol {tol}, floor {floor:.3g}, "
                           f"worst error/bound {worst:.3f})")
+    if not check_ml:
+        return report
     if dtype == "fp32":
         assert np.all(err_m <= 1e-5 + 1e-5 * np.abs(m_ref)), f"{label}: m beyond all_close, max {err_m.max():.3g}"
         assert np.all(err_l <= 1e-5 + 1e-5 * np.abs(l_ref)), f"{label}: l beyond all_close, max {err_l.max():.3g}"

@@ -42,7 +42,7 @@ def _np(t):
     return t.detach().to("cpu", torch.float32).numpy().astype(np.float64)
 
 
-def _run(B, H, S, D, dtype, causal, seed, with_o=False, dist="normal", heads=None):
+def _run(B, H, S, D, dtype, causal, seed, with_o=False, dist="normal", heads=None, ml_dtype=None):
     import torch
 
     import pmkl_amd
@@ -52,7 +52,7 @@ def _run(B, H, S, D, dtype, causal, seed, with_o=False, dist="normal", heads=Non
     rng = np.random.Generator(np.random.PCG64(seed + 17))
     do = torch.from_numpy(rng.standard_normal((B, H, S, D)).astype(np.float32)).to(torch_dtype(dtype))
     qd, kd, vd, dod = (x.to("cuda:0") for x in (q, k, v, do))
-    o, m, l = pmkl_amd.attn_fwd(qd, kd, vd, is_causal=causal)
+    o, m, l = pmkl_amd.attn_fwd(qd, kd, vd, is_causal=causal, ml_dtype=ml_dtype)
     dq, dk, dv = pmkl_amd.attn_bwd(dod, qd, kd, vd, m, l, is_causal=causal, out=o if with_o else None)
     torch.cuda.synchronize()
     r = lambda t: _np(t).reshape(B * H, S, D)
@@ -128,6 +128,17 @@ def test_bwd_with_forward_output(device, dtype):
         _say(f"case {tag}")
         got, ref, fl = _run(2, 2, 300, 64, dtype, causal, seed=400, with_o=True)
         _check(got, ref, dtype, tag, fl)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_bwd_float_ml_from_64_row_kernel(device, dtype, causal):
+    """m and l in float32 from the 64-row forward kernel (head_dim 128,
+    S > 128) feed the backward, which reads them as float32."""
+    tag = f"bwd {dtype} float m/l D=128 causal={causal} B1 H2 S300"
+    _say(f"case {tag}")
+    got, ref, fl = _run(1, 2, 300, 128, dtype, causal, seed=450, ml_dtype=__import__("torch").float32)
+    _check(got, ref, dtype, tag, fl)
 
 
 def test_bwd_larger_heads_sampled(device):

@@ -75,26 +75,37 @@ def test_small_shapes_vs_oracle(device, dtype, D, causal):
         check_outputs(q, k, v, o, m, l, dtype, causal=causal, label=tag)
 
 
+# (S, D, causal) of the float m/l cases: S 200 at head_dim 64 runs the 8-wave
+# kernel in its resident form; head_dim 128 from S 129 and causal head_dim 64
+# from S 512 run the 64-row kernel, whose epilogue has its own float m/l store.
+ML_F32_SHAPES = [(200, 64, True), (300, 128, True), (300, 128, False), (1024, 64, True)]
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
-def test_ml_float32_output(device, dtype):
+@pytest.mark.parametrize("S,D,causal", ML_F32_SHAPES)
+def test_ml_float32_output(device, dtype, S, D, causal):
     """ml_dtype = F32 returns m and l without rounding them to the tensor dtype.
     m is the fp32 row max (1e-5).  l is the sum of the probabilities as rounded
     to the tensor dtype for the P*V product (the weights O is normalised by),
     so it sits within the relative rounding of those probabilities of the
-    exact sum: 2^-8 for bf16, 2^-11 for fp16."""
+    exact sum: 2^-8 for bf16, 2^-11 for fp16.  O meets the usual bound."""
     import torch
     from oracle import oracle
     from pmkl_amd.workloads import small_inputs
-    from tests.parity import to_np
+    from tests.parity import check_outputs, to_np
 
-    q, k, v = small_inputs(2, 2, 200, 64, dtype, seed=7)
-    o, m, l = _run_capi(q, k, v, device, ml_dtype=torch.float32)
+    _say(f"case ml f32 {dtype} B2 H2 S{S} D{D} causal={causal}")
+    q, k, v = small_inputs(2, 2, S, D, dtype, seed=7 + S + D)
+    o, m, l = _run_capi(q, k, v, device, causal=causal, ml_dtype=torch.float32)
     assert m.dtype == torch.float32 and l.dtype == torch.float32
-    qn, kn, vn = (to_np(x).reshape(4, 200, 64) for x in (q, k, v))
-    _, m_ref, l_ref = oracle.attn_fwd_rows(qn, kn, vn)
-    assert np.allclose(to_np(m).reshape(4, 200), m_ref, rtol=1e-5, atol=1e-5)
+    qn, kn, vn = (to_np(x).reshape(4, S, D) for x in (q, k, v))
+    _, m_ref, l_ref = oracle.attn_fwd_rows(qn, kn, vn, causal=causal)
+    assert np.allclose(to_np(m).reshape(4, S), m_ref, rtol=1e-5, atol=1e-5)
     rel = {"bf16": 2.0 ** -8, "fp16": 2.0 ** -11}[dtype]
-    assert np.all(np.abs(to_np(l).reshape(4, 200) - l_ref) <= rel * l_ref)
+    assert np.all(np.abs(to_np(l).reshape(4, S) - l_ref) <= rel * l_ref)
+    # O against the oracle; m and l checked above in float32
+    check_outputs(q, k, v, o, m.to(q.dtype), l.to(q.dtype), dtype, causal=causal,
+                  label=f"ml f32 S{S} D{D}", check_ml=False)
 
 
 def test_reference_test_shape_fp32(device):
