@@ -489,11 +489,19 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     };
     const int mode = w64_mode();
     const bool causal = a->is_causal != 0;
-    const bool w64 = mode != 0 && (mode == 1 || D >= 128 || (D == 64 && causal && S >= 512)) &&
+    // Head_dim 128 with fewer 256-row work items than CUs (most CUs idle
+    // under the 64-row kernel) at 128 < S <= 384 (causal: 192 < S <= 352):
+    // the 4-wave MFMA kernel, whose 128-row workgroups spread the rows over
+    // twice as many CUs (measured 3-16% faster there; slower once the items
+    // fill the CUs, and for causal rows outside that range with very few
+    // heads; PMKL_ATTN_W64=1 keeps the 64-row kernel).
+    const bool small128 = mode != 1 && D == 128 && (causal ? S > 192 && S <= 352 : S > 128 && S <= 384) &&
+                          B * H * ((S + 255) / 256) < (int64_t)cu_count();
+    const bool w64 = mode != 0 && !small128 && (mode == 1 || D >= 128 || (D == 64 && causal && S >= 512)) &&
                      a->dtype != PMKL_DTYPE_F32 && S > 128 && head_span_ok(ks) && head_span_ok(vs);
     const bool w32 = w64 && (D == 64 || D == 128) && w32_mode() == 1;
     const bool bf = a->dtype == PMKL_DTYPE_BF16;
-    const int waves = waves16(D, S, causal);
+    const int waves = small128 && !waves16_env() ? 4 : waves16(D, S, causal);
     const bool resident = !w64 && a->dtype != PMKL_DTYPE_F32 && waves == 8 &&
                           (S + 63) / 64 <= resident_tiles(D) && resident_enabled();
     const bool split = w32 && D == 64 && causal && split_enabled() &&

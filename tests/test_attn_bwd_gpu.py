@@ -134,10 +134,10 @@ def test_bwd_with_forward_output(device, dtype):
 @pytest.mark.parametrize("causal", [True, False])
 def test_bwd_float_ml_from_64_row_kernel(device, dtype, causal):
     """m and l in float32 from the 64-row forward kernel (head_dim 128,
-    S > 128) feed the backward, which reads them as float32."""
-    tag = f"bwd {dtype} float m/l D=128 causal={causal} B1 H2 S300"
+    S > 384) feed the backward, which reads them as float32."""
+    tag = f"bwd {dtype} float m/l D=128 causal={causal} B1 H2 S520"
     _say(f"case {tag}")
-    got, ref, fl = _run(1, 2, 300, 128, dtype, causal, seed=450, ml_dtype=__import__("torch").float32)
+    got, ref, fl = _run(1, 2, 520, 128, dtype, causal, seed=450, ml_dtype=__import__("torch").float32)
     _check(got, ref, dtype, tag, fl)
 
 

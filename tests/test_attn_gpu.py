@@ -76,9 +76,10 @@ def test_small_shapes_vs_oracle(device, dtype, D, causal):
 
 
 # (S, D, causal) of the float m/l cases: S 200 at head_dim 64 runs the 8-wave
-# kernel in its resident form; head_dim 128 from S 129 and causal head_dim 64
-# from S 512 run the 64-row kernel, whose epilogue has its own float m/l store.
-ML_F32_SHAPES = [(200, 64, True), (300, 128, True), (300, 128, False), (1024, 64, True)]
+# kernel in its resident form, head_dim 128 at S 300 (few work items) its
+# 4-wave streaming form; head_dim 128 from S 385 and causal head_dim 64 from
+# S 512 run the 64-row kernel, whose epilogue has its own float m/l store.
+ML_F32_SHAPES = [(200, 64, True), (300, 128, True), (520, 128, True), (520, 128, False), (1024, 64, True)]
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
