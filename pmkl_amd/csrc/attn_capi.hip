@@ -158,6 +158,15 @@ bool split_enabled() {
     }();
     return on;
 }
+// fp32 problems too small to fill the CUs take the key-split kernel unless
+// PMKL_ATTN_F32SPLIT=0 (read once).
+bool f32split_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("PMKL_ATTN_F32SPLIT");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
 
 // split: causal head_dim 64 with fewer 256-row work items than two per CU
 // runs two 128-row workgroups per CU instead (measured same-box: B1 H8 S8192
@@ -183,6 +192,19 @@ KernelChoice pick32(bool causal) {
     return {causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, true>
                    : (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, false>,
             pmkl_amd::kThreads, pmkl_amd::kBlockM};
+}
+
+template <int D>
+KernelChoice pick32split(bool causal) {
+    return {causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_split_kernel<D, true>
+                   : (kernel_fn)pmkl_amd::attn_fwd_f32_split_kernel<D, false>,
+            256, 32};
+}
+KernelChoice pick32split(int64_t d, bool causal) {
+    if (d == 32) return pick32split<32>(causal);
+    if (d == 64) return pick32split<64>(causal);
+    if (d == 128) return pick32split<128>(causal);
+    return {nullptr, 0, 0};
 }
 
 KernelChoice select_kernel(int32_t dt, int64_t d, bool causal, bool w64, int waves, bool resident) {
@@ -506,8 +528,13 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
                           (S + 63) / 64 <= resident_tiles(D) && resident_enabled();
     const bool split = w32 && D == 64 && causal && split_enabled() &&
                        B * H * ((S + 255) / 256) < 2 * (int64_t)cu_count();
-    const KernelChoice kc = w32 ? (bf ? pick_w32<__bf16>(D, causal, split) : pick_w32<_Float16>(D, causal, split))
-                                : select_kernel(a->dtype, D, causal, w64, waves, resident);
+    // fp32 with the 128-row kernel's workgroups on fewer than half the CUs
+    // (C1: 4): 32-row workgroups whose four waves split the key tiles.
+    const bool f32split = a->dtype == PMKL_DTYPE_F32 && f32split_enabled() && S <= 1024 &&
+                          B * H * ((S + 127) / 128) * 2 < (int64_t)cu_count();
+    const KernelChoice kc = w32        ? (bf ? pick_w32<__bf16>(D, causal, split) : pick_w32<_Float16>(D, causal, split))
+                            : f32split ? pick32split(D, causal)
+                                       : select_kernel(a->dtype, D, causal, w64, waves, resident);
     PMKL_REQUIRE(kc.fn != nullptr, PMKL_EUNSUPPORTED, "no kernel for dtype %d head_dim %lld", (int)a->dtype,
                  (long long)D);
     const int64_t n_qtiles = (S + kc.block_m - 1) / kc.block_m;

@@ -675,4 +675,191 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(AttnParams p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp32, small problems: one workgroup per (head, 32-row query block); its
+// NSPL waves split the block's key tiles (wave w takes tiles w, w + NSPL,
+// ...), each staging its own tiles in LDS (no workgroup barrier in the loop),
+// then the partial (O, m, l) of the waves are combined by the log-sum-exp
+// rule.  The rows' longest chain of dependent tiles shrinks NSPL-fold, which
+// is what bounds a launch of a few workgroups.  Same arithmetic per tile as
+// attn_fwd_f32_kernel (v_mfma_f32_32x32x2f32, exact rescale).
+// ---------------------------------------------------------------------------
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void attn_fwd_f32_split_kernel(AttnParams p) {
+    constexpr int BN = 32;            // keys per tile (= query rows per workgroup)
+    constexpr int NSPL = 4;           // waves, each a share of the key tiles
+    constexpr int LD = D + 1;         // padded LDS row (floats)
+    constexpr int NDB = D / 32;
+    constexpr int NDK = D / 2;
+    constexpr int NE = BN * D / 64;   // elements per lane per tensor per tile
+    // Per wave: K and V tile; after the loop the same memory holds the
+    // partials (NDB * 16 accumulators + m + l per lane and wave).
+    constexpr int PW = NDB * 16 * 64 + 2 * 64;
+    static_assert(NSPL * PW <= NSPL * 2 * BN * LD, "partials fit the staging memory");
+    __shared__ float smem[NSPL * 2 * BN * LD];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int col = lane & 31;
+
+    const int L = blockIdx.x;
+    const int bh = L % p.BH;
+    const int rb = CAUSAL ? (p.n_qtiles - 1 - L / p.BH) : (L / p.BH);
+    const int b = bh / p.H;
+    const int h = bh - b * p.H;
+    const int S = p.S;
+
+    const float *qg = (const float *)p.q + b * p.q_sb + h * p.q_sh;
+    const float *kg = (const float *)p.k + b * p.k_sb + h * p.k_sh;
+    const float *vg = (const float *)p.v + b * p.v_sb + h * p.v_sh;
+    float *og = (float *)p.o + b * p.o_sb + h * p.o_sh;
+
+    const int q0 = rb * BN;
+    const int qi = q0 + col;
+    // Every row of the block sees at least the first key of each tile up to
+    // its block's diagonal tile (rows and key tiles are both 32 wide).
+    const int last_key = CAUSAL ? min(q0 + BN - 1, S - 1) : S - 1;
+    const int nt = last_key / BN + 1;
+
+    float qf[NDK];
+    {
+        const int qrow = min(qi, S - 1);
+        const float *src = qg + (int64_t)qrow * p.q_ss + hi;
+#pragma unroll
+        for (int dk = 0; dk < NDK; ++dk) qf[dk] = src[2 * dk];
+    }
+    f32x16_t acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const int arow = key_of_arow(col);
+    float *Ks = smem + wave * 2 * BN * LD;
+    float *Vs = Ks + BN * LD;
+
+    for (int kt = wave; kt < nt; kt += NSPL) {
+        const int kbase = kt * BN;
+        float kreg[NE], vreg[NE];
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            const int i = j * 64 + lane;
+            const int r = i / D, c = i % D;
+            const int key = min(kbase + r, S - 1);
+            kreg[j] = kg[(int64_t)key * p.k_ss + c];
+            vreg[j] = vg[(int64_t)key * p.v_ss + c];
+        }
+        // The wave's own LDS region: its earlier reads of the previous tile
+        // are issued before these writes, and the LDS executes one wave's
+        // instructions in order, so neither side needs a barrier.
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            const int i = j * 64 + lane;
+            const int r = i / D, c = i % D;
+            Ks[r * LD + c] = kreg[j];
+            Vs[r * LD + c] = vreg[j];
+        }
+        asm volatile("" ::: "memory");
+        f32x16_t sacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+#pragma unroll
+        for (int dk = 0; dk < NDK; ++dk)
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[arow * LD + 2 * dk + hi], qf[dk], sacc, 0, 0, 0);
+        const bool need_mask = (CAUSAL && kbase + BN - 1 > q0) || (kbase + BN > S);
+        if (need_mask) {
+            const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (kbase + 16 * hi + r > lim) sacc[r] = -INFINITY;
+        }
+        float mx = sacc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+        mx = half_max(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = fast_exp2((m_run - m_use) * p.scale_log2);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        const float moff = -m_use * p.scale_log2;
+        float pr[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pr[r] = fast_exp2(__builtin_fmaf(sacc[r], p.scale_log2, moff));
+            l_run += pr[r];
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+                acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(16 * hi + c) * LD + 32 * db + col], pr[c], acc[db],
+                                                                0, 0, 0);
+        asm volatile("" ::: "memory");
+    }
+
+    // Partials to LDS (the staging memory, once every wave is past its loop),
+    // then wave 0 combines them: O = sum_w 2^((m_w - M) c) O_w over the
+    // block's running maxima M = max_w m_w, l likewise.  A wave without
+    // tiles holds m = -inf, l = 0, O = 0 and weighs 0.
+    __syncthreads();
+    float *part = smem + wave * PW;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[(db * 16 + r) * 64 + lane] = acc[db][r];
+    part[NDB * 1024 + lane] = m_run;
+    part[NDB * 1024 + 64 + lane] = l_run;
+    __syncthreads();
+    if (wave != 0) return;
+    float mw[NSPL];
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NSPL; ++w) {
+        mw[w] = smem[w * PW + NDB * 1024 + lane];
+        M = fmaxf(M, mw[w]);
+    }
+    float l_sum = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+#pragma unroll
+    for (int w = 0; w < NSPL; ++w) {
+        const float f = fast_exp2((mw[w] - M) * p.scale_log2);   // 0 for a wave without tiles
+        const float *pw = smem + w * PW;
+        l_sum += f * pw[NDB * 1024 + 64 + lane];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][r] += f * pw[(db * 16 + r) * 64 + lane];
+    }
+    const float l_tot = half_sum(l_sum);
+    if (qi < S) {
+        const float inv = 1.0f / l_tot;
+        float *orow = og + (int64_t)qi * p.o_ss;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * db + 8 * g4 + 4 * hi;
+                float4 w4 = {acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv, acc[db][4 * g4 + 2] * inv,
+                             acc[db][4 * g4 + 3] * inv};
+                *(float4 *)(orow + d) = w4;
+            }
+        if (hi == 0) {
+            const int64_t mi = (int64_t)bh * S + qi;
+            ((float *)p.m)[mi] = M * p.scale;
+            ((float *)p.l)[mi] = l_tot;
+        }
+    }
+}
+
 }  // namespace pmkl_amd

@@ -24,7 +24,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     shapes = [(1, 3, 300, 128, "bf16", True), (2, 2, 257, 128, "fp16", False), (1, 2, 520, 64, "bf16", True),
               (2, 2, 200, 32, "fp16", True), (1, 5, 1000, 128, "bf16", True), (3, 2, 256, 64, "fp16", True),
-              (2, 2, 128, 128, "bf16", False), (1, 2, 129, 128, "fp16", True), (2, 1, 384, 128, "bf16", False)]
+              (2, 2, 128, 128, "bf16", False), (1, 2, 129, 128, "fp16", True), (2, 1, 384, 128, "bf16", False),
+              (1, 4, 128, 64, "fp32", True), (2, 1, 300, 128, "fp32", False), (1, 2, 33, 32, "fp32", True)]
     env = {k: v for k, v in os.environ.items() if k.startswith("PMKL_ATTN")}
     for i, (B, H, S, D, dt, causal) in enumerate(shapes):
         tag = f"{env} {dt} B{B} H{H} S{S} D{D} causal={causal}"

@@ -1,8 +1,8 @@
 """The kernel-choice switches of the C ABI (PMKL_ATTN_W32, PMKL_ATTN_W64,
-PMKL_ATTN_WAVES, PMKL_ATTN_NOXCD, PMKL_ATTN_RESIDENT, PMKL_ATTN_SPLIT) change which kernel runs, never the
+PMKL_ATTN_WAVES, PMKL_ATTN_NOXCD, PMKL_ATTN_RESIDENT, PMKL_ATTN_SPLIT, PMKL_ATTN_F32SPLIT) change which kernel runs, never the
 results' definition: each setting runs tests/switch_check.py in a child
 process (the library reads the switches once per process), which compares a
-few 16-bit shapes with the float64 oracle."""
+few shapes with the float64 oracle."""
 from __future__ import annotations
 
 import os
@@ -24,6 +24,7 @@ SETTINGS = [
     {"PMKL_ATTN_NOXCD": "1"},                        # plain (head, tile) work order
     {"PMKL_ATTN_RESIDENT": "0"},                     # short sequences on the streaming 8-wave kernel
     {"PMKL_ATTN_SPLIT": "0"},                        # small causal head_dim-64 problems on 256-row workgroups
+    {"PMKL_ATTN_F32SPLIT": "0"},                     # small fp32 problems on the 128-row fp32 kernel
 ]
 
 
