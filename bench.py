@@ -40,18 +40,36 @@ METRIC = "causal-attn TFLOP/s on 1 MI355X, bf16 B4 H32 S4096 D128; % of MFMA pea
 
 def kernel_name(w) -> str:
     """Kernel the C ABI dispatches for the causal workload w (its dispatch
-    rule, restated for the bench line's label): fp32 -> the fp32 kernel;
-    16-bit -> the 64-row kernel for S > 128 at head_dim 128, and at head_dim
-    64 from S = 512 on, unless PMKL_ATTN_W64=0 (=1 takes it at every head_dim
-    for S > 128), else the 4- or 8-wave MFMA kernel."""
+    rule, restated for the bench line's label): fp32 -> the key-split fp32
+    kernel where the 128-row fp32 kernel would occupy fewer than half the CUs
+    (S <= 1024; unless PMKL_ATTN_F32SPLIT=0), else the 128-row one; 16-bit ->
+    the 64-row kernel for S > 128 at head_dim 128 (except problems with fewer
+    256-row items than CUs at 192 < S <= 352), and at head_dim 64 from S = 512
+    on, unless PMKL_ATTN_W64=0 (=1 takes it at every head_dim for S > 128),
+    else the 4- or 8-wave MFMA kernel."""
+    cus = _cu_count()
     if w.dtype == "fp32":
-        return "attn_fwd_f32_kernel"
+        split = (os.environ.get("PMKL_ATTN_F32SPLIT") != "0" and w.S <= 1024
+                 and w.B * w.H * (-(-w.S // 128)) * 2 < cus)
+        return "attn_fwd_f32_split_kernel" if split else "attn_fwd_f32_kernel"
     mode = os.environ.get("PMKL_ATTN_W64")
     if mode is None:
-        w64 = w.D >= 128 or (w.D == 64 and w.S >= 512)
+        small128 = w.D == 128 and 192 < w.S <= 352 and w.B * w.H * (-(-w.S // 256)) < cus
+        w64 = (w.D >= 128 and not small128) or (w.D == 64 and w.S >= 512)
     else:
         w64 = mode == "1"
     return "attn_fwd_w64_kernel" if w64 and w.S > 128 else "attn_fwd_mfma16_kernel"
+
+
+def _cu_count() -> int:
+    """CUs of device 0 (256 on MI355X when no GPU is visible)."""
+    import torch
+
+    if torch.cuda.is_available():
+        return torch.cuda.get_device_properties(0).multi_processor_count
+    return 256
+
+
 WARMUP_MIN_S = 1.0
 
 
