@@ -109,6 +109,32 @@ def test_ml_float32_output(device, dtype, S, D, causal):
                   label=f"ml f32 S{S} D{D}", check_ml=False)
 
 
+# fp32 on both sides of the host's key-split rule (the 128-row fp32 kernel's
+# workgroups on fewer than half the CUs and S <= 1024 -> 32-row workgroups
+# whose waves split the key tiles): (B, H, S, D, causal, rows sampled).
+F32_RULE_SHAPES = [
+    (1, 1, 1024, 64, True, False),    # split kernel at its largest S, 32 key tiles over 4 waves
+    (1, 1, 1025, 64, True, False),    # one past: the 128-row kernel
+    (1, 3, 700, 128, False, False),   # split kernel, non-causal, ragged
+    (4, 40, 384, 64, True, True),     # 480 workgroups of 128 rows: the 128-row kernel
+    (2, 8, 200, 32, True, False),     # split kernel, head_dim 32, ragged
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,causal,sampled", F32_RULE_SHAPES)
+def test_fp32_both_kernels(device, B, H, S, D, causal, sampled):
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+
+    tag = f"fp32 B{B} H{H} S{S} D{D} causal={causal}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, "fp32", seed=7500 + S + H)
+    o, m, l = _run_capi(q, k, v, device, causal=causal)
+    rows = _sample_rows(S, 16, seed=S) if sampled else None
+    errs = check_outputs(q, k, v, o, m, l, "fp32", causal=causal, rows=rows, label=tag)
+    _say(f"{tag}: {errs}")
+
+
 def test_reference_test_shape_fp32(device):
     """The reference's GPU test: {4,16,1024,64} fp32, U(-1.05,1.05), all_close 1e-5."""
     from pmkl_amd.workloads import small_inputs
