@@ -370,6 +370,30 @@ def test_strided_bshd_inputs(device):
     assert torch.equal(o, ref[0])
 
 
+@pytest.mark.parametrize("B,H,S,D", [(1, 3, 200, 64), (2, 2, 131, 128)])
+def test_strided_bshd_fp32_against_oracle(device, B, H, S, D):
+    """fp32 (the key-split kernel at these sizes): q/k/v as [B, S, H, D]
+    memory viewed as [B, H, S, D], and the output written through a strided
+    [B, S, H, D] view, against the oracle; equal bit for bit to the
+    contiguous call."""
+    import torch
+    import pmkl_amd
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+
+    tag = f"fp32 strided B{B} H{H} S{S} D{D}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, "fp32", seed=7600 + S)
+    qs, ks, vs = (x.transpose(1, 2).contiguous().to(device).transpose(1, 2) for x in (q, k, v))
+    assert not qs.is_contiguous()
+    ob = torch.empty((B, S, H, D), dtype=q.dtype, device=device).transpose(1, 2)
+    o, m, l = pmkl_amd.attn_fwd(qs, ks, vs, is_causal=True, out=ob)
+    torch.cuda.synchronize()
+    check_outputs(q, k, v, o, m, l, "fp32", causal=True, label=tag)
+    ref = _run_capi(q, k, v, device)
+    assert all(torch.equal(x, y) for x, y in zip(ref, (o, m, l)))
+
+
 def test_output_canaries(device):
     """Nothing is written outside O, m, l: guard regions before and after stay
     intact, and poisoned (NaN) outputs are fully overwritten."""
