@@ -109,6 +109,31 @@ def test_ml_float32_output(device, dtype, S, D, causal):
                   label=f"ml f32 S{S} D{D}", check_ml=False)
 
 
+# 16-bit head_dim 128 on both sides of the host's small-problem rule (fewer
+# 256-row work items than CUs at S <= 384, causal 192 < S <= 352 -> the
+# 4-wave kernel, else the 64-row kernel): (B, H, S, dtype, causal).
+D128_RULE_SHAPES = [
+    (2, 4, 192, "bf16", True), (2, 4, 193, "fp16", True),        # causal lower edge
+    (2, 4, 352, "bf16", True), (2, 4, 353, "fp16", True),        # causal upper edge
+    (2, 4, 384, "fp16", False), (2, 4, 385, "bf16", False),      # non-causal upper edge
+    (1, 255, 256, "bf16", True), (1, 256, 256, "bf16", True),    # 255 vs 256 work items
+]
+
+
+@pytest.mark.parametrize("B,H,S,dtype,causal", D128_RULE_SHAPES)
+def test_head_dim128_rule_edges(device, B, H, S, dtype, causal):
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+
+    tag = f"{dtype} B{B} H{H} S{S} D128 causal={causal}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, 128, dtype, seed=7700 + S + H)
+    o, m, l = _run_capi(q, k, v, device, causal=causal)
+    rows = _sample_rows(S, 16, seed=S) if B * H > 64 else None
+    errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)
+    _say(f"{tag}: {errs}")
+
+
 # fp32 on both sides of the host's key-split rule (the 128-row fp32 kernel's
 # workgroups on fewer than half the CUs and S <= 1024 -> 32-row workgroups
 # whose waves split the key tiles): (B, H, S, D, causal, rows sampled).
