@@ -50,7 +50,8 @@
 // DMAs of iteration t-1 (K(t+2), V(t+1)).  So a DMA only overwrites a slot
 // all waves have finished reading (K(t-1), V(t-2), read before the previous
 // barrier), and a tile is read only after the barrier that follows its
-// arrival.
+// arrival.  At head_dim 64 (PAIR below) barriers come at odd positions only,
+// with the same DMAs issued in each position's first slots.
 #pragma once
 
 #include "attn_fwd_kernels.hpp"
