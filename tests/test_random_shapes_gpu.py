@@ -58,3 +58,44 @@ def test_random_shape_forward_and_backward(device, case):
     ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), mn, ln, causal=causal)
     fl = _term_floors(r(q), r(k), r(v), r(do), mn, ln, causal) if dtype == "fp32" else (0.0, 0.0, 0.0)
     _say(f"  {_check([r(dq), r(dk), r(dv)], ref, dtype, tag, fl)}")
+
+
+N_MANY = 12
+
+
+def _many_head_cases(seed=20261203, n=N_MANY):
+    """Many heads (B 2-8, H 16-40) at S 129-1,100: the other side of the
+    small-problem kernel rules (several work items per workgroup of the 64-row
+    kernel, the fp32 kernel of 128-row workgroups)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(n):
+        S = int(np.round(np.exp(rng.uniform(np.log(129.0), np.log(1100.0)))))
+        out.append(dict(B=int(rng.integers(2, 9)), H=int(rng.integers(16, 41)), S=S,
+                        D=int(rng.choice([64, 128])), dtype=str(rng.choice(["bf16", "fp16", "fp32"])),
+                        causal=bool(rng.integers(0, 2)), seed=7200 + i))
+    return out
+
+
+@pytest.mark.parametrize("case", _many_head_cases(), ids=lambda c: "B{B}H{H}S{S}D{D}-{dtype}-{c}".format(
+    c="causal" if c["causal"] else "full", **{k: v for k, v in c.items() if k != "causal"}))
+def test_random_shape_forward_many_heads(device, case):
+    """Forward only, every head, sampled rows (first, last, tile edges and 8
+    random ones) against the float64 oracle."""
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+    from tests.test_attn_bwd_gpu import _say
+
+    B, H, S, D, dtype, causal = (case[k] for k in ("B", "H", "S", "D", "dtype", "causal"))
+    tag = f"random many heads B{B} H{H} S{S} D{D} {dtype} causal={causal} seed={case['seed']}"
+    _say(f"case {tag}")
+    q, k, v = small_inputs(B, H, S, D, dtype, seed=case["seed"])
+    o, m, l = pmkl_amd.attn_fwd(q.to("cuda:0"), k.to("cuda:0"), v.to("cuda:0"), is_causal=causal)
+    torch.cuda.synchronize()
+    rng = np.random.Generator(np.random.PCG64(case["seed"]))
+    fixed = [0, 1, 63, 64, 127, 128, 255, 256, S // 2, S - 65, S - 64, S - 1]
+    rows = sorted(set(r for r in fixed + rng.choice(S, size=8, replace=False).tolist() if 0 <= r < S))
+    _say(f"  {check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)}")
