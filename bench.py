@@ -10,9 +10,14 @@ headline metric is quoted on.  Prints one JSON line.
              pairs; softmax not counted)
   roofline   the attention kernel against the dense bf16 MFMA peak
              (2,516.6 TFLOP/s): achieved = FLOPs per launch / average launch
-             duration from HIP events on the launch stream; traffic = HBM bytes
-             per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
-             + WRITE_SIZE, scaled by a copy-kernel calibration), or null
+             duration from HIP events on the launch stream; kernel = the one the
+             library's dispatcher chose (pmkl_attn_fwd_kernel_name); launches =
+             median / min / max of 64 launches timed one by one after the timed
+             region; traffic = HBM bytes per launch from the committed
+             rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by a
+             copy-kernel calibration), or null; profile = the committed
+             rocprofv3 kernel-trace means of this kernel (one per lease, with
+             the shader clock of that lease) and the fraction they give
   cpu_baseline  the reference's own CPU operator (oracle/_ref, compiled from
              pmkl_pytorch_ext/fused_self_attention.cpp) on a bounded sample:
              one head per core on all usable cores at once (value), and one
@@ -38,39 +43,8 @@ PEAK_HBM_GBS = 8000.0
 METRIC = "causal-attn TFLOP/s on 1 MI355X, bf16 B4 H32 S4096 D128; % of MFMA peak"
 
 
-def kernel_name(w) -> str:
-    """Kernel the C ABI dispatches for the causal workload w (its dispatch
-    rule, restated for the bench line's label): fp32 -> the key-split fp32
-    kernel where the 128-row fp32 kernel would occupy fewer than half the CUs
-    (S <= 1024; unless PMKL_ATTN_F32SPLIT=0), else the 128-row one; 16-bit ->
-    the 64-row kernel for S > 128 at head_dim 128 (except problems with fewer
-    256-row items than CUs at 192 < S <= 352), and at head_dim 64 from S = 512
-    on, unless PMKL_ATTN_W64=0 (=1 takes it at every head_dim for S > 128),
-    else the 4- or 8-wave MFMA kernel."""
-    cus = _cu_count()
-    if w.dtype == "fp32":
-        split = (os.environ.get("PMKL_ATTN_F32SPLIT") != "0" and w.S <= 1024
-                 and w.B * w.H * (-(-w.S // 128)) * 2 < cus)
-        return "attn_fwd_f32_split_kernel" if split else "attn_fwd_f32_kernel"
-    mode = os.environ.get("PMKL_ATTN_W64")
-    if mode is None:
-        small128 = w.D == 128 and 192 < w.S <= 352 and w.B * w.H * (-(-w.S // 256)) < cus
-        w64 = (w.D >= 128 and not small128) or (w.D == 64 and w.S >= 512)
-    else:
-        w64 = mode == "1"
-    return "attn_fwd_w64_kernel" if w64 and w.S > 128 else "attn_fwd_mfma16_kernel"
-
-
-def _cu_count() -> int:
-    """CUs of device 0 (256 on MI355X when no GPU is visible)."""
-    import torch
-
-    if torch.cuda.is_available():
-        return torch.cuda.get_device_properties(0).multi_processor_count
-    return 256
-
-
 WARMUP_MIN_S = 1.0
+LAUNCH_SAMPLES = 64
 
 
 def parse_args():
@@ -112,16 +86,42 @@ def calibrate_copy():
 def read_traffic(config: str, kernel: str, name: str | None = None):
     """HBM bytes per launch from profiles/pmc_attn_fwd_<config>.txt (or
     profiles/<name>) when that summary was measured on `kernel` (its
-    "kernel_id:" line), else None."""
+    "kernel_id:" line equals the kernel's name up to its launch shape), else
+    None."""
     path = ROOT / "profiles" / (name or f"pmc_attn_fwd_{config}.txt")
     if not path.exists():
         return None
     txt = path.read_text()
-    k = re.search(r"^kernel_id:\s*(\S+)", txt, re.M)
-    if k is None or k.group(1) != kernel:
+    k = re.search(r"^kernel_id:\s*(.+?)\s*$", txt, re.M)
+    if k is None or k.group(1) != kernel.split(" grid")[0]:
         return None
     m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
     return float(m.group(1)) if m else None
+
+
+def read_profile(config: str, kernel: str, flops: float, peak: float):
+    """The committed kernel traces of `kernel` at `config`
+    (profiles/attn_fwd_w64_<config>_kernel_trace.txt): one "lease:" line per
+    fresh GPU lease with the trace mean of the timed dispatches (us) and the
+    shader clock of that lease; returns them with the fraction of peak they
+    give, or None when no summary was taken on this kernel."""
+    path = ROOT / "profiles" / f"attn_fwd_w64_{config}_kernel_trace.txt"
+    if not path.exists():
+        return None
+    txt = path.read_text()
+    k = re.search(r"^kernel_id:\s*(.+?)\s*$", txt, re.M)
+    if k is None or k.group(1) != kernel.split(" grid")[0]:
+        return None
+    leases = [{"lease": m.group(1), "trace_mean_us": float(m.group(2)), "shader_clock_GHz": float(m.group(3))}
+              for m in re.finditer(r"^lease:\s*(\S+)\s+trace_mean_us\s+([0-9.]+)\s+shader_clock_GHz\s+([0-9.]+)",
+                                   txt, re.M)]
+    if not leases:
+        return None
+    best = min(x["trace_mean_us"] for x in leases)
+    mean = sum(x["trace_mean_us"] for x in leases) / len(leases)
+    return {"file": str(path.relative_to(ROOT)), "leases": leases,
+            "frac_best_lease": round(flops / (best / 1e6) / 1e12 / peak, 4),
+            "frac_mean_of_leases": round(flops / (mean / 1e6) / 1e12 / peak, 4)}
 
 
 def _host_cpu():
@@ -155,27 +155,49 @@ def _run_cpu_workers(npz: str, heads):
     result), or None if a worker failed."""
     import subprocess
 
+    import queue
+    import threading
+
     procs = [subprocess.Popen([sys.executable, "-m", "oracle.cpu_baseline", npz, str(h)], cwd=str(ROOT),
                               stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True) for h in heads]
+    # Each worker's lines arrive through a reader thread, so that every wait
+    # has a deadline: a worker that hangs costs the CPU leg, never the line.
+    lines = [queue.Queue() for _ in procs]
+
+    def reader(p, q):
+        for ln in p.stdout:
+            q.put(ln)
+        q.put(None)
+
+    for p, q in zip(procs, lines):
+        threading.Thread(target=reader, args=(p, q), daemon=True).start()
+    deadline = time.perf_counter() + CPU_WORKER_TIMEOUT_S
+
+    def next_line(q):
+        ln = q.get(timeout=max(0.0, deadline - time.perf_counter()))
+        if ln is None:
+            raise ValueError("worker ended")
+        return ln
+
     try:
-        for p in procs:
-            if p.stdout.readline().strip() != "ready":
+        for q in lines:
+            if next_line(q).strip() != "ready":
                 return None
         t0 = time.perf_counter()
         for p in procs:
             p.stdin.write("go\n")
             p.stdin.flush()
         secs = []
-        for p in procs:
-            r = json.loads(p.stdout.readline())
+        for q in lines:
+            r = json.loads(next_line(q))
             if "seconds" not in r:
                 return None
             secs.append(r["seconds"])
         wall = time.perf_counter() - t0
         for p in procs:
-            p.wait(timeout=CPU_WORKER_TIMEOUT_S)
+            p.wait(timeout=max(1.0, deadline - time.perf_counter()))
         return secs, wall
-    except (ValueError, OSError):
+    except (ValueError, OSError, queue.Empty, subprocess.TimeoutExpired):
         return None
     finally:
         for p in procs:
@@ -542,6 +564,17 @@ def main():
     gpu_ms = ev0.elapsed_time(ev1)
     avg_launch_ms = gpu_ms / args.steps
 
+    # Per-launch statistics, after the timed region: each of LAUNCH_SAMPLES
+    # launches between its own pair of events on the launch stream.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(LAUNCH_SAMPLES)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    per_launch_us = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+
     flops = causal_flops(w.B, w.H, w.S, w.D)
     esize = {"bf16": 2, "fp16": 2, "fp32": 4}[w.dtype]
     alg_bytes = (4 * w.B * w.H * w.S * w.D + 2 * w.B * w.H * w.S) * esize
@@ -549,7 +582,8 @@ def main():
     value = flops * args.steps / elapsed_s / 1e12
     achieved = flops / (avg_launch_ms / 1e3) / 1e12
     peak = PEAK_TFLOPS[w.dtype]
-    traffic = read_traffic(w.name, kernel_name(w))
+    kernel = capi.attn_fwd_kernel_name(cargs)
+    traffic = read_traffic(w.name, kernel)
 
     cpu = None if args.no_cpu else cpu_baseline(w)
     sdpa = torch_sdpa_reference(q, k, v, flops, min(args.steps, 20)) if args.sdpa else None
@@ -574,8 +608,14 @@ def main():
         "pct_of_mfma_peak": round(100.0 * value / peak, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4), "traffic": traffic,
-                     "kernel": kernel_name(w),
+                     "kernel": kernel,
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
+                     "launches": {"n": len(per_launch_us),
+                                  "median_us": round(per_launch_us[len(per_launch_us) // 2], 2),
+                                  "min_us": round(per_launch_us[0], 2), "max_us": round(per_launch_us[-1], 2),
+                                  "frac_at_median": round(flops / (per_launch_us[len(per_launch_us) // 2] / 1e6)
+                                                          / 1e12 / peak, 4)},
+                     "profile": read_profile(w.name, kernel, flops, peak),
                      "hbm_GBs_algorithmic": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9, 1)},
         "cpu_baseline": cpu,
         "torch_sdpa": sdpa,

@@ -30,7 +30,10 @@
  *   - The caller allocates every tensor (and the backward's workspace) in
  *     device memory; the library allocates nothing per call.
  *   - Calls are asynchronous on the given stream (NULL = the default stream).
- *   - The functions are re-entrant and thread-safe; error text is thread-local.
+ *   - The functions are re-entrant and thread-safe, with one exception:
+ *     pmkl_attn_bwd_noalloc keeps its scratch in one array per GPU, so calls
+ *     of it that overlap on one GPU race (see its declaration).  Error text is
+ *     thread-local.
  */
 #ifndef PMKL_ATTN_H_
 #define PMKL_ATTN_H_
@@ -41,7 +44,7 @@
 extern "C" {
 #endif
 
-#define PMKL_ABI_VERSION 4
+#define PMKL_ABI_VERSION 5
 
 /* Element types.  The reference dispatches on float, double, half and
  * bfloat16 (fused_self_attention.cpp:152-156); the device path implements
@@ -100,6 +103,17 @@ int pmkl_causal_attention_forward(int32_t dtype, void *out, const void *q, const
 
 /* 1 if a kernel is compiled for (dtype, head_dim), else 0. */
 int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim);
+
+/* The kernel pmkl_attn_fwd would launch for these arguments, with its launch
+ * shape and work order, e.g.
+ * "attn_fwd_w64_kernel<bf16, 128, causal, 1, 8> grid 256 x 512, xcd order";
+ * "none" for an empty problem; NULL (and pmkl_last_error() text) where
+ * pmkl_attn_fwd would return an error.  Launches nothing.  The string lives in
+ * thread-local storage until the calling thread's next call of this function.
+ * No counterpart in the reference: it labels measurements (the reference's
+ * launcher times each launch, pmkl/core/launcher/cuda_launcher.h:317-328,
+ * without naming what it ran).  ABI version 5. */
+const char *pmkl_attn_fwd_kernel_name(const pmkl_attn_fwd_args *args);
 
 /* Arguments of pmkl_attn_bwd.  Tensors [B, H, S, D] with head_dim contiguous
  * and any batch / head / seq element strides (all three zero: contiguous), as

@@ -46,6 +46,9 @@ def _check_fwd_buffers(q, out, out_m, out_l, ml_dtype):
             raise ValueError(f"out must be a [{B}, {H}, {S}, {D}] {q.dtype} tensor on {q.device}")
         if out.stride(3) != 1:
             raise ValueError("out: head_dim must be contiguous")
+        if _rows_overlap(_abi_strides(out), (B, H, S), D):
+            raise ValueError(f"out strides {tuple(out.stride())} make distinct rows overlap "
+                             "(an expanded or aliased output)")
     mdt = ml_dtype
     for name, t in (("out_m", out_m), ("out_l", out_l)):
         if t is None:
@@ -102,6 +105,22 @@ def attn_fwd(q, k, v, is_causal: bool = True, scale: float | None = None, ml_dty
     if rc != capi.PMKL_OK:
         raise capi.PmklError(rc, capi.last_error())
     return out, out_m, out_l
+
+
+def _rows_overlap(strides, sizes, D) -> bool:
+    """True unless distinct rows (b, h, s) of a [B, H, S, D] layout with these
+    batch / head / seq element strides (head_dim contiguous) are sure not to
+    share an element: with the dimensions of size > 1 sorted by stride, each
+    stride must be at least the extent of the dimensions inside it (D
+    elements for the innermost).  The C ABI applies the same rule to outputs."""
+    extent = D
+    for st, n in sorted(zip(strides, sizes)):
+        if n <= 1:
+            continue
+        if st < extent:
+            return True
+        extent = st * (n - 1) + extent
+    return False
 
 
 def _abi_strides(t):

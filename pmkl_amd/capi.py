@@ -27,6 +27,7 @@ PMKL_ATTN_BWD_NOALLOC_MAX_ROWS = 1048576   # include/pmkl_attn.h
 # Every symbol include/pmkl_attn.h and include/pmkl_softmax.h declare.
 EXPORTED_SYMBOLS = (
     "pmkl_attn_fwd",
+    "pmkl_attn_fwd_kernel_name",
     "pmkl_causal_attention_forward",
     "pmkl_attn_fwd_supported",
     "pmkl_attn_bwd_workspace_size",
@@ -143,6 +144,8 @@ def load() -> ctypes.CDLL:
         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
     ]
     lib.pmkl_causal_attention_forward.restype = ctypes.c_int
+    lib.pmkl_attn_fwd_kernel_name.argtypes = [ctypes.POINTER(AttnFwdArgs)]
+    lib.pmkl_attn_fwd_kernel_name.restype = ctypes.c_char_p
     lib.pmkl_attn_fwd_supported.argtypes = [ctypes.c_int32, ctypes.c_int64]
     lib.pmkl_attn_fwd_supported.restype = ctypes.c_int
     lib.pmkl_last_error.argtypes = []
@@ -179,6 +182,14 @@ def last_error() -> str:
 def attn_fwd_raw(args: AttnFwdArgs, stream: int | None = None) -> int:
     """Call pmkl_attn_fwd; returns the status code."""
     return load().pmkl_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream or 0))
+
+
+def attn_fwd_kernel_name(args: AttnFwdArgs) -> str | None:
+    """The kernel (and launch shape) pmkl_attn_fwd would launch for args, as
+    the library's dispatcher chooses it; None where the call would fail
+    (last_error() says why)."""
+    name = load().pmkl_attn_fwd_kernel_name(ctypes.byref(args))
+    return None if name is None else name.decode()
 
 
 def make_args(q, k, v, o, m, l, *, dtype: int, ml_dtype: int | None = None, batch: int, heads: int,

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <utility>
 
 #include "pmkl_attn.h"
 #include "capi_common.hpp"
@@ -53,12 +54,16 @@ bool head_dim_supported(int64_t d) { return d == 32 || d == 64 || d == 128; }
 using pmkl_amd::AttnParams;
 typedef void (*kernel_fn)(AttnParams);
 
-// A kernel and its launch shape: threads per workgroup and query rows per workgroup.
+// A kernel and its launch shape: threads per workgroup and query rows per
+// workgroup; family and t1, t2 (its template parameters after the mask, -1
+// if none) name it for pmkl_attn_fwd_kernel_name.
 struct KernelChoice {
     kernel_fn fn;
     int threads;
     int block_m;
     int per_cu = 1;   // persistent workgroups per CU (64-row kernel)
+    const char *family = "";
+    int t1 = -1, t2 = -1;
 };
 
 // PMKL_ATTN_WAVES=4 or 8 pins the waves of the 16-bit MFMA kernel; 0 if unset.
@@ -82,7 +87,7 @@ template <typename T, int D, int NW, int NTR = 0>
 KernelChoice pick16w(bool causal) {
     return {causal ? (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, true, NW, NTR>
                    : (kernel_fn)pmkl_amd::attn_fwd_mfma16_kernel<T, D, false, NW, NTR>,
-            NW * 64, NW * 32};
+            NW * 64, NW * 32, 1, "attn_fwd_mfma16_kernel", NW, NTR};
 }
 // Key tiles (of 64) the resident form of the 8-wave kernel holds in LDS:
 // NTR * 2 * 64 * D * 2 bytes, 32 KiB at head_dim 32, 64 KiB at 64 and 128.
@@ -147,7 +152,7 @@ template <typename T, int D>
 KernelChoice pick_w32(bool causal) {
     return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, true, 1, 8>
                    : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false, 1, 8>,
-            512, 256};
+            512, 256, 1, "attn_fwd_w64_kernel", 1, 8};
 }
 // Two 128-row workgroups per CU for small causal head_dim-64 problems unless
 // PMKL_ATTN_SPLIT=0 (read once).
@@ -174,7 +179,8 @@ bool f32split_enabled() {
 // two or more 256-row items per CU).
 template <typename T>
 KernelChoice pick_w32(int64_t D, bool causal, bool split) {
-    if (D == 64 && causal && split) return {(kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 64, true, 1, 4>, 256, 128, 2};
+    if (D == 64 && causal && split)
+        return {(kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, 64, true, 1, 4>, 256, 128, 2, "attn_fwd_w64_kernel", 1, 4};
     return D == 64 ? pick_w32<T, 64>(causal) : pick_w32<T, 128>(causal);
 }
 
@@ -183,7 +189,7 @@ KernelChoice pick16(bool causal, bool w64, int waves, bool resident) {
     if (w64)
         return {causal ? (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, true>
                        : (kernel_fn)pmkl_amd::attn_fwd_w64_kernel<T, D, false>,
-                256, 256};
+                256, 256, 1, "attn_fwd_w64_kernel", 2, 4};
     if (resident) return pick16w<T, D, 8, resident_tiles(D)>(causal);
     return waves == 4 ? pick16w<T, D, 4>(causal) : pick16w<T, D, 8>(causal);
 }
@@ -191,14 +197,14 @@ template <int D>
 KernelChoice pick32(bool causal) {
     return {causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, true>
                    : (kernel_fn)pmkl_amd::attn_fwd_f32_kernel<D, false>,
-            pmkl_amd::kThreads, pmkl_amd::kBlockM};
+            pmkl_amd::kThreads, pmkl_amd::kBlockM, 1, "attn_fwd_f32_kernel"};
 }
 
 template <int D>
 KernelChoice pick32split(bool causal) {
     return {causal ? (kernel_fn)pmkl_amd::attn_fwd_f32_split_kernel<D, true>
                    : (kernel_fn)pmkl_amd::attn_fwd_f32_split_kernel<D, false>,
-            256, 32};
+            256, 32, 1, "attn_fwd_f32_split_kernel"};
 }
 KernelChoice pick32split(int64_t d, bool causal) {
     if (d == 32) return pick32split<32>(causal);
@@ -263,6 +269,25 @@ int check_tensor(const char *name, const void *ptr, const int64_t st[3], int64_t
     return PMKL_OK;
 }
 
+// An output must not alias itself: distinct (b, h, s) rows of a [B, H, S, D]
+// tensor (head_dim contiguous) must not share an element, or workgroups
+// writing different rows race on the same bytes.  Sufficient test: with the
+// dimensions of size > 1 sorted by stride, each stride is at least the extent
+// of the dimensions inside it (D elements for the innermost).
+int check_no_self_overlap(const char *name, const int64_t st[3], int64_t B, int64_t H, int64_t S, int64_t D) {
+    std::pair<int64_t, int64_t> dims[3] = {{st[0], B}, {st[1], H}, {st[2], S}};   // (stride, size)
+    std::sort(dims, dims + 3);
+    double extent = (double)D;
+    for (const auto &d : dims) {
+        if (d.second <= 1) continue;
+        PMKL_REQUIRE((double)d.first >= extent, PMKL_EINVAL,
+                     "%s strides (%lld, %lld, %lld) make distinct rows of the output overlap", name,
+                     (long long)st[0], (long long)st[1], (long long)st[2]);
+        extent = (double)d.first * (double)(d.second - 1) + extent;
+    }
+    return PMKL_OK;
+}
+
 using pmkl_amd::BwdParams;
 typedef void (*bwd_kernel_fn)(BwdParams);
 
@@ -317,6 +342,7 @@ struct BwdTensorArg {
     const void *ptr;
     const int64_t *strides;
     bool optional;   // may be null (o)
+    bool output;     // written by the call (dq, dk, dv)
 };
 
 // Validates a backward call except for the workspace.  *empty is set for a
@@ -342,16 +368,17 @@ int check_bwd(const pmkl_attn_bwd_args *a, bool *empty) {
     PMKL_REQUIRE(B * H * S * D < (1LL << 62), PMKL_EINVAL, "tensors span too many elements");
     const size_t es = dtype_size(a->dtype);
     const BwdTensorArg tensors[] = {
-        {"dout", a->dout, a->dout_strides, false}, {"q", a->q, a->q_strides, false},
-        {"k", a->k, a->k_strides, false},          {"v", a->v, a->v_strides, false},
-        {"o", a->o, a->o_strides, true},           {"dq", a->dq, a->dq_strides, false},
-        {"dk", a->dk, a->dk_strides, false},       {"dv", a->dv, a->dv_strides, false}};
+        {"dout", a->dout, a->dout_strides, false, false}, {"q", a->q, a->q_strides, false, false},
+        {"k", a->k, a->k_strides, false, false},          {"v", a->v, a->v_strides, false, false},
+        {"o", a->o, a->o_strides, true, false},           {"dq", a->dq, a->dq_strides, false, true},
+        {"dk", a->dk, a->dk_strides, false, true},        {"dv", a->dv, a->dv_strides, false, true}};
     int rc;
     for (const auto &t : tensors) {
         if (t.ptr == nullptr && t.optional) continue;
         int64_t st[3];
         default_strides(st, t.strides, H, S, D);
         if ((rc = check_tensor(t.name, t.ptr, st, B, H, S, D, es)) != PMKL_OK) return rc;
+        if (t.output && (rc = check_no_self_overlap(t.name, st, B, H, S, D)) != PMKL_OK) return rc;
     }
     PMKL_REQUIRE(a->m != nullptr && a->l != nullptr, PMKL_EINVAL, "m / l must not be null");
     const size_t ml_es = dtype_size(a->ml_dtype);
@@ -460,20 +487,18 @@ int scratch_on_device(float **out) {
     return PMKL_OK;
 }
 
-}  // namespace
+// A validated forward call: kernel, grid and parameters.
+struct FwdPlan {
+    KernelChoice kc;
+    AttnParams p;
+    int64_t grid;
+    bool empty;
+};
 
-extern "C" {
-
-const char *pmkl_last_error(void) { return pmkl_capi::g_err; }
-
-int pmkl_abi_version(void) { return PMKL_ABI_VERSION; }
-
-int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim) {
-    return dtype_valid(dtype) && head_dim_supported(head_dim) ? 1 : 0;
-}
-
-int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
-    pmkl_capi::g_err[0] = '\0';
+// Validates a forward call and chooses its kernel, launch shape and
+// parameters (pl->empty: no rows, nothing to launch).
+int plan_fwd(const pmkl_attn_fwd_args *a, FwdPlan *pl) {
+    pl->empty = false;
     PMKL_REQUIRE(a != nullptr, PMKL_EINVAL, "args is a null pointer");
     PMKL_REQUIRE(dtype_valid(a->dtype), PMKL_EUNSUPPORTED, "unsupported dtype %d", (int)a->dtype);
     PMKL_REQUIRE(a->ml_dtype == a->dtype || a->ml_dtype == PMKL_DTYPE_F32, PMKL_EINVAL,
@@ -485,7 +510,10 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
                  "head_dim %lld has no compiled kernel (supported: 32, 64, 128)", (long long)a->head_dim);
     PMKL_REQUIRE(std::isfinite(a->scale) && a->scale >= 0.f, PMKL_EINVAL, "scale must be finite and >= 0");
     // Empty problem: nothing to do (reference causal_attention.h:270).
-    if (a->batch * a->heads * a->seq_len == 0) return PMKL_OK;
+    if (a->batch * a->heads * a->seq_len == 0) {
+        pl->empty = true;
+        return PMKL_OK;
+    }
 
     const int64_t B = a->batch, H = a->heads, S = a->seq_len, D = a->head_dim;
     PMKL_REQUIRE(S <= (1LL << 30) && B * H <= (1LL << 30), PMKL_EINVAL, "shape too large (B*H %lld, S %lld)",
@@ -501,6 +529,7 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     if ((rc = check_tensor("k", a->k, ks, B, H, S, D, es)) != PMKL_OK) return rc;
     if ((rc = check_tensor("v", a->v, vs, B, H, S, D, es)) != PMKL_OK) return rc;
     if ((rc = check_tensor("o", a->o, os, B, H, S, D, es)) != PMKL_OK) return rc;
+    if ((rc = check_no_self_overlap("o", os, B, H, S, D)) != PMKL_OK) return rc;
 
     // The 64-row kernel addresses a head's whole K / V through one buffer
     // resource with 32-bit offsets, and streams the first key tiles of its
@@ -545,7 +574,7 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     PMKL_REQUIRE((uintptr_t)a->m % ml_es == 0 && (uintptr_t)a->l % ml_es == 0, PMKL_EINVAL,
                  "m / l must be aligned to their element size");
 
-    AttnParams p;
+    AttnParams &p = pl->p;
     p.q = a->q;
     p.k = a->k;
     p.v = a->v;
@@ -567,7 +596,6 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
     // XCD-grouped issue order needs whole head pairs (causal) or heads per XCD.
     p.xcd_order = (a->dtype != PMKL_DTYPE_F32 && xcd_order_enabled() && (B * H) % (a->is_causal ? 16 : 8) == 0) ? 1 : 0;
 
-    hipStream_t st = (hipStream_t)stream;
     // One workgroup per work item, except the 64-row kernel: one workgroup per
     // CU, each looping over its share of the items.
     int64_t grid = n_qtiles * B * H;
@@ -576,10 +604,51 @@ int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
         PMKL_REQUIRE(cus > 0, PMKL_EHIP, "could not read the device's CU count");
         grid = std::min<int64_t>(grid, (int64_t)kc.per_cu * cus);
     }
-    hipLaunchKernelGGL(kc.fn, dim3((unsigned)grid), dim3(kc.threads), 0, st, p);
+    pl->kc = kc;
+    pl->grid = grid;
+    return PMKL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *pmkl_last_error(void) { return pmkl_capi::g_err; }
+
+int pmkl_abi_version(void) { return PMKL_ABI_VERSION; }
+
+int pmkl_attn_fwd_supported(int32_t dtype, int64_t head_dim) {
+    return dtype_valid(dtype) && head_dim_supported(head_dim) ? 1 : 0;
+}
+
+int pmkl_attn_fwd(const pmkl_attn_fwd_args *a, void *stream) {
+    pmkl_capi::g_err[0] = '\0';
+    FwdPlan pl;
+    const int rc = plan_fwd(a, &pl);
+    if (rc != PMKL_OK || pl.empty) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(pl.kc.fn, dim3((unsigned)pl.grid), dim3(pl.kc.threads), 0, st, pl.p);
     hipError_t err = hipGetLastError();
     PMKL_REQUIRE(err == hipSuccess, PMKL_EHIP, "kernel launch failed: %s", hipGetErrorString(err));
     return PMKL_OK;
+}
+
+const char *pmkl_attn_fwd_kernel_name(const pmkl_attn_fwd_args *a) {
+    pmkl_capi::g_err[0] = '\0';
+    static thread_local char name[160];
+    FwdPlan pl;
+    if (plan_fwd(a, &pl) != PMKL_OK) return nullptr;
+    if (pl.empty) return "none";
+    const char *dt = a->dtype == PMKL_DTYPE_BF16 ? "bf16" : a->dtype == PMKL_DTYPE_F16 ? "fp16" : "fp32";
+    const char *mask = a->is_causal ? "causal" : "full";
+    const char *order = pl.p.xcd_order ? ", xcd order" : "";
+    if (pl.kc.t1 >= 0)
+        snprintf(name, sizeof(name), "%s<%s, %lld, %s, %d, %d> grid %lld x %d%s", pl.kc.family, dt,
+                 (long long)a->head_dim, mask, pl.kc.t1, pl.kc.t2, (long long)pl.grid, pl.kc.threads, order);
+    else
+        snprintf(name, sizeof(name), "%s<%lld, %s> grid %lld x %d%s", pl.kc.family, (long long)a->head_dim, mask,
+                 (long long)pl.grid, pl.kc.threads, order);
+    return name;
 }
 
 uint64_t pmkl_attn_bwd_workspace_size(int64_t batch, int64_t heads, int64_t seq_len) {

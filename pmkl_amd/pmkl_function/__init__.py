@@ -13,8 +13,9 @@ Dispatch:
   * anything else -> NotImplementedError, as in the reference.
 Backward (gradients of out only; those of out_m, out_l are ignored, as in the
 reference, __init__.py:25-32): CPU with debug=True -> fused_self_attention_bw's
-CPU body, as the reference; ROCm fp16 / bf16 tensors -> pmkl_attn_bwd (the
-gfx950 backward), given the saved forward output so its row terms come from
+CPU body, as the reference; ROCm float32 / float16 / bfloat16 tensors ->
+pmkl_attn_bwd (the gfx950 backward: vector-ALU kernels for float32, MFMA for
+the 16-bit types), given the saved forward output so its row terms come from
 <dout, out>; anything else -> NotImplementedError.
 """
 import torch

@@ -191,10 +191,28 @@ def _sample_rows(S, n_random, seed):
     return sorted(set(r for r in fixed + rnd if 0 <= r < S))
 
 
+# Heads (flattened b * H + h) checked on every row at the full-size configs:
+# the first and last head and one in the middle (C3: batch 1 head 31).
+FULL_HEADS = {"C3": (0, 63, 127), "C4": (0, 15)}
+
+
+def check_full_heads(q, k, v, o, m, l, dtype, heads, label):
+    """Every row of the given flattened heads against the oracle, as the
+    reference's GPU test checks every element (test/test_causal_attention.cpp:197-204)."""
+    from tests.parity import check_outputs
+
+    B, H, S, D = q.shape
+    idx = list(heads)
+    sel = lambda t, shape: t.reshape(B * H, *shape)[idx].reshape(1, len(idx), *shape)   # noqa: E731
+    return check_outputs(sel(q, (S, D)), sel(k, (S, D)), sel(v, (S, D)), sel(o.cpu(), (S, D)),
+                         sel(m.cpu(), (S,)), sel(l.cpu(), (S,)), dtype, label=label)
+
+
 @pytest.mark.parametrize("name", ["C3", "C4"])
 def test_config_sampled_rows(device, name):
-    """Full-size C3 / C4: every head, a fixed set of rows (tile edges, first and
-    last rows, random rows) against the oracle."""
+    """Full-size C3 / C4: every row of three (C3) / two (C4) whole heads, and in
+    every head a fixed set of rows (tile edges, first and last rows, random
+    rows), against the oracle."""
     from pmkl_amd.workloads import WORKLOADS, torch_dtype, host_inputs
     from tests.parity import check_outputs
     import torch
@@ -203,6 +221,8 @@ def test_config_sampled_rows(device, name):
     _say(f"config {name} {w.shape} {w.dtype}")
     q, k, v = (torch.from_numpy(a).to(torch_dtype(w.dtype)) for a in host_inputs(w))
     o, m, l = _run_capi(q, k, v, device)
+    errs = check_full_heads(q, k, v, o, m, l, w.dtype, FULL_HEADS[name], label=f"{name} full heads")
+    _say(f"{name}: all rows of heads {FULL_HEADS[name]} {errs}")
     rows = _sample_rows(w.S, 24 if name == "C3" else 12, seed=w.seed)
     errs = check_outputs(q, k, v, o, m, l, w.dtype, rows=rows, label=name)
     _say(f"{name}: rows {len(rows)} {errs}")

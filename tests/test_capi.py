@@ -40,7 +40,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_abi_version_and_support_matrix():
     lib = capi.load()
-    assert lib.pmkl_abi_version() == 4
+    assert lib.pmkl_abi_version() == 5
     for dt in (capi.PMKL_DTYPE_F32, capi.PMKL_DTYPE_F16, capi.PMKL_DTYPE_BF16):
         for d in (32, 64, 128):
             assert lib.pmkl_attn_fwd_supported(dt, d) == 1
@@ -78,6 +78,11 @@ def test_error_paths():
     _expect(_args(q_strides=(2 * 64 * 64, 64 * 64, 68)), capi.PMKL_EINVAL, "multiples of 8 elements")
     _expect(_args(o_strides=(1 << 40, 1 << 30, 1 << 28)), capi.PMKL_EINVAL, "too large")
     _expect(_args(m=0), capi.PMKL_EINVAL, "m / l must not be null")
+    # outputs whose rows alias (an expanded batch, heads packed closer than a head's rows)
+    _expect(_args(batch=2, o_strides=(0, 64 * 64, 64)), capi.PMKL_EINVAL, "o strides .* overlap")
+    _expect(_args(o_strides=(2 * 64 * 64, 32 * 64, 64)), capi.PMKL_EINVAL, "o strides .* overlap")
+    # interleaved heads ([B, S, H, D] memory) do not overlap: the call plans a kernel
+    assert capi.attn_fwd_kernel_name(_args(o_strides=(2 * 64 * 64, 64, 2 * 64))) is not None, capi.last_error()
     _expect(_args(dtype=capi.PMKL_DTYPE_F32, ml_dtype=capi.PMKL_DTYPE_F32, m=0x5002), capi.PMKL_EINVAL,
             "aligned to their element size")
 
@@ -174,6 +179,10 @@ def test_bwd_error_paths():
     _expect_bwd(_bwd_args(strides={"dq": (2 * 64 * 72, 72, 2 * 72 + 4)}), capi.PMKL_EINVAL,
                 r"dq strides .* must be multiples of 8 elements")
     _expect_bwd(_bwd_args(strides={"dout": (-1, 64, 128)}), capi.PMKL_EINVAL, "dout strides")
+    # gradient outputs whose rows alias
+    _expect_bwd(_bwd_args(strides={"dk": (2 * 64 * 64, 0, 64)}), capi.PMKL_EINVAL, "dk strides .* overlap")
+    _expect_bwd(_bwd_args(strides={"dv": (2 * 64 * 64, 64 * 32, 64)}), capi.PMKL_EINVAL, "dv strides .* overlap")
+    _expect_bwd(_bwd_args(batch=2, strides={"dq": (0, 64 * 64, 64)}), capi.PMKL_EINVAL, "dq strides .* overlap")
     with pytest.raises(ValueError, match="no stride field"):
         _bwd_args(strides={"m": (0, 0, 1)})
     # an empty problem succeeds without touching anything
@@ -273,7 +282,33 @@ def test_attn_fwd_rejects_bad_output_buffers():
         ((None, ok_m, None, torch.float32), "out_m is torch.bfloat16"),
         ((None, torch.empty(2, 3, 40, dtype=torch.float16), None, None), "m/l dtype must be"),
         ((None, torch.empty(2, 3, 40, dtype=q.dtype, device="meta"), None, None), "out_m must be"),
+        # outputs whose rows alias: expanded over batch, over heads, rows closer than head_dim
+        ((torch.empty(1, 3, 40, 64, dtype=q.dtype).expand(2, 3, 40, 64), None, None, None), "overlap"),
+        ((torch.empty(2, 1, 40, 64, dtype=q.dtype).expand(2, 3, 40, 64), None, None, None), "overlap"),
+        ((torch.empty(2 * 3 * 40 * 64, dtype=q.dtype).as_strided((2, 3, 40, 64), (3 * 40 * 64, 40 * 32, 32, 1)),
+          None, None, None), "overlap"),
     ]
     for (o, m, l, mdt), msg in bad:
         with pytest.raises(ValueError, match=msg):
             _check_fwd_buffers(q, o, m, l, mdt)
+
+
+def test_kernel_name_query():
+    """pmkl_attn_fwd_kernel_name names the kernel pmkl_attn_fwd would launch,
+    or returns NULL with the same error text where the call would fail; it
+    launches nothing (shapes here need no device to plan)."""
+    # an invalid call: NULL and the check's text
+    assert capi.attn_fwd_kernel_name(_args(head_dim=80)) is None
+    assert "head_dim 80" in capi.last_error()
+    assert capi.attn_fwd_kernel_name(_args(o_strides=(0, 64 * 64, 64), batch=2)) is None
+    assert "overlap" in capi.last_error()
+    # an empty problem launches nothing
+    assert capi.attn_fwd_kernel_name(_args(seq_len=0, q=0, k=0, v=0, o=0, m=0, l=0)) == "none"
+    # short 16-bit sequences: the resident form of the 8-wave MFMA kernel
+    name = capi.attn_fwd_kernel_name(_args(seq_len=200))
+    assert name.startswith("attn_fwd_mfma16_kernel<bf16, 64, causal, 8, 4> grid "), name
+    assert capi.attn_fwd_kernel_name(_args(seq_len=200, is_causal=False)).startswith(
+        "attn_fwd_mfma16_kernel<bf16, 64, full, 8, 4>")
+    # fp32 with the CU count unknown (no device): the 128-row fp32 kernel
+    name = capi.attn_fwd_kernel_name(_args(dtype=capi.PMKL_DTYPE_F32, ml_dtype=capi.PMKL_DTYPE_F32, seq_len=300))
+    assert name == "attn_fwd_f32_kernel<64, causal> grid 6 x 256", name

@@ -53,11 +53,13 @@ def _sample_rows(S, n_random, seed):
 @pytest.mark.parametrize("name", ["C1", "C2", "C5", "C3"])
 def test_torch_op_and_autograd_forward_vs_oracle(device, name):
     """fused_self_attention_fw and fused_self_attention (device branch) at a
-    benchmark configuration: all rows (C3: every head, sampled rows)."""
+    benchmark configuration: all rows (C3: every row of heads 0, 63 and 127,
+    and sampled rows of every head)."""
     import torch
     import pmkl_pytorch_ext
     from pmkl_function import fused_self_attention
     from tests.parity import check_outputs
+    from tests.test_attn_gpu import FULL_HEADS, check_full_heads
 
     w, q, k, v = _config_inputs(name)
     rows = _sample_rows(w.S, 24, seed=w.seed) if name == "C3" else None
@@ -68,12 +70,20 @@ def test_torch_op_and_autograd_forward_vs_oracle(device, name):
     assert o.dtype == m.dtype == l.dtype == q.dtype and o.is_contiguous()
     errs = check_outputs(q, k, v, o, m, l, w.dtype, rows=rows, label=f"{name} fused_self_attention_fw")
     _say(f"PARITY {name} fused_self_attention_fw {errs}")
+    if name == "C3":
+        errs = check_full_heads(q, k, v, o, m, l, w.dtype, FULL_HEADS[name],
+                                label=f"{name} fused_self_attention_fw full heads")
+        _say(f"PARITY {name} fused_self_attention_fw all rows of heads {FULL_HEADS[name]} {errs}")
     del o, m, l
     _say(f"config {name}: pmkl_function.fused_self_attention")
     o, m, l = fused_self_attention(qd, kd, vd, True)
     torch.cuda.synchronize()
     errs = check_outputs(q, k, v, o, m, l, w.dtype, rows=rows, label=f"{name} fused_self_attention")
     _say(f"PARITY {name} fused_self_attention {errs}")
+    if name == "C3":
+        errs = check_full_heads(q, k, v, o, m, l, w.dtype, FULL_HEADS[name],
+                                label=f"{name} fused_self_attention full heads")
+        _say(f"PARITY {name} fused_self_attention all rows of heads {FULL_HEADS[name]} {errs}")
 
 
 @pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
