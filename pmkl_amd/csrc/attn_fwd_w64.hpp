@@ -546,13 +546,17 @@ void attn_fwd_w64_kernel(AttnParams p) {
             }
         }
     };
-    float mx[QB], mh[QB];
-    // Max unit k of score set SET: k < 4 QB partial row max (qb, kb, half);
-    // k in [4 QB, 5 QB) the row max of block k - 4 QB (both lane halves);
-    // k in [5 QB, 6 QB) the update of block k - 5 QB: exact running max and
-    // the lazy rescale decision, without branches (the O rescale itself waits
-    // for the PV MFMAs in flight).  Split so that no dependency chain stalls
-    // the in-order issue for long.
+    float mx[QB];
+    bool upv[QB];
+    // Max unit k of score set SET: k < 4 QB partial row max (qb, kb, half) of
+    // the lane's own keys; k in [4 QB, 5 QB) for block k - 4 QB the lane's
+    // running max (m_true holds each lane's half of a row; the two halves
+    // are combined once per item, in the epilogue) and whether its tile max
+    // passes the lazy threshold; k in [5 QB, 6 QB) the rescale decision for
+    // block k - 5 QB (a wave-uniform branch, taken rarely): the row max over
+    // both lane halves, the new offset and the factor for O and l (the O
+    // rescale itself waits for the PV MFMAs in flight).  Split so that no
+    // dependency chain stalls the in-order issue for long.
     auto max_unit = [&](auto set_c, int k) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
         if (k < 4 * QB) {
@@ -573,19 +577,18 @@ void attn_fwd_w64_kernel(AttnParams p) {
             mx[qb] = m;
         } else if (k < 5 * QB) {
             const int qb = k - 4 * QB;
-            mh[qb] = half_max(mx[qb]);
-            asm volatile("" : "+v"(mh[qb]));
+            m_true[qb] = w64_max(m_true[qb], mx[qb]);
+            upv[qb] = mx[qb] > m_use[qb] + lazy_raw;
         } else {
             const int qb = k - 5 * QB;
-            const float m = mh[qb];
-            m_true[qb] = fmaxf(m_true[qb], m);
-            const bool up = __builtin_amdgcn_ballot_w64(m > m_use[qb] + lazy_raw) != 0;
-            const float m_new = fmaxf(m_use[qb], m);
-            alpha[qb] = fast_exp2((m_use[qb] - m_new) * p.scale_log2);   // read only when up; 0 on the first tile
-            const float mo = m_new == -INFINITY ? 0.f : -m_new * p.scale_log2;
-            rescale[qb] = up;
-            m_use[qb] = up ? m_new : m_use[qb];
-            moff[qb] = up ? mo : moff[qb];
+            if (__builtin_amdgcn_ballot_w64(upv[qb]) != 0) {
+                const float mh = half_max(mx[qb]);
+                const float m_new = fmaxf(m_use[qb], mh);
+                alpha[qb] = fast_exp2((m_use[qb] - m_new) * p.scale_log2);   // 0 on the first tile
+                moff[qb] = m_new == -INFINITY ? 0.f : -m_new * p.scale_log2;
+                m_use[qb] = m_new;
+                rescale[qb] = true;
+            }
         }
     };
     // The O^T accumulators and row sums of block qb at a drain.
@@ -729,11 +732,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
                     const u32x4_t w4 = {r0[0], r1[0], r0[1], r1[1]};
                     if (ok) *(u32x4_t *)(orow + 32 * db + 16 * j + 8 * hi) = w4;
                 }
+            const float m_row = half_max(m_true[qb]);   // both lane halves of the row
             if (ok) {
-                const float l_tot = l_sum * fast_exp2((m_use[qb] - m_true[qb]) * p.scale_log2);
+                const float l_tot = l_sum * fast_exp2((m_use[qb] - m_row) * p.scale_log2);
                 if (hi == 0) {
                     const int64_t mi = (int64_t)bh_e * S + qi;
-                    const float mval = m_true[qb] * p.scale;
+                    const float mval = m_row * p.scale;
                     if (p.ml_f32) {
                         ((float *)p.m)[mi] = mval;
                         ((float *)p.l)[mi] = l_tot;
