@@ -355,9 +355,29 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     const int vrow0 = 16 * (g >> 1) + (tt >> 2);
     const int vcol0 = 16 * (g & 1) + 4 * (tt & 3);
 
+    // Causal resident form at head_dim 32: a wave's rows start on a 32-key
+    // block boundary, so each 32-key block is wholly visible, wholly masked,
+    // or the diagonal block, whose mask is the same for every wave: lane
+    // half hi, register r holds key 16 hi + r of the block against query col.
+    // The diagonal block takes its mask as the accumulator input of its first
+    // score MFMA (0 where visible, -inf where not), which costs no VALU work
+    // (a compare and a select per score otherwise); the masked block after it
+    // is skipped.  The mask lives in LDS (dtab[j][lane] = registers 4j ..
+    // 4j+3 of lane; wave 0 writes it before the workgroup's barrier), read
+    // with four conflict-free 16-byte reads: kept in VGPRs it is rebuilt by
+    // the compiler on every use.  Only at head_dim 32: the extra registers
+    // of the three tile bodies would cost waves per SIMD at 64 and 128.
+    constexpr bool BIAS = CAUSAL && NTR > 0 && D == 32;
+    __shared__ __attribute__((aligned(16))) f32x4_t dtab[BIAS ? 4 * 64 : 1];
+
     // One key tile kt of this wave from LDS stage st: scores, mask, online
-    // softmax, O update.
-    auto compute_tile = [&](int st, int kt) __attribute__((always_inline)) {
+    // softmax, O update.  KIND 0: element-wise mask where the tile straddles
+    // the diagonal or the end of the sequence; 1: no mask; 2: diagonal block
+    // second (BIAS only); 3: diagonal block first, second block masked
+    // (BIAS only).
+    auto compute_tile = [&](int st, int kt, auto kind_c) __attribute__((always_inline)) {
+        constexpr int KIND = decltype(kind_c)::value;
+        constexpr int NKB = KIND == 3 ? 1 : 2;   // 32-key blocks computed
         const int kbase = kt * BN;
         {
             const T *Ks = smem[st][0];
@@ -365,9 +385,25 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             // ---- S^T = K Q^T for two 32-key blocks ----
             f32x16_t sacc[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
+                if constexpr (BIAS && (KIND == 2 || KIND == 3)) {
+                    if (kb == (KIND == 2 ? 1 : 0)) {
+                        const f32x4_t b0 = dtab[lane], b1 = dtab[64 + lane], b2 = dtab[128 + lane], b3 = dtab[192 + lane];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+                        for (int e = 0; e < 4; ++e) {
+                            sacc[kb][e] = b0[e];
+                            sacc[kb][4 + e] = b1[e];
+                            sacc[kb][8 + e] = b2[e];
+                            sacc[kb][12 + e] = b3[e];
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+                }
                 const int row = 32 * kb + arow;
                 const T *krow = Ks + row * D;
                 const int sw = swz_k<CPR>(row);
@@ -380,7 +416,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             }
             // ---- mask (only tiles that straddle the diagonal or the end) ----
             const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
-            if (need_mask) {
+            if (KIND == 0 && need_mask) {
                 const int lim = CAUSAL ? min(qi, S - 1) : S - 1;   // last visible key
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
@@ -392,11 +428,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                 }
             }
             // ---- online softmax ----
-            float mx = sacc[0][0];
+            // Row max as a tree (v_max3, depth 3 per block) rather than a
+            // 16-deep chain: the chain's latency sits between the score
+            // MFMAs and the exponentials of every tile.
+            float bm[NKB];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb) {
+                float t5[5];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+                for (int i = 0; i < 5; ++i) t5[i] = fmaxf(fmaxf(sacc[kb][3 * i], sacc[kb][3 * i + 1]), sacc[kb][3 * i + 2]);
+                bm[kb] = fmaxf(fmaxf(fmaxf(t5[0], t5[1]), t5[2]), fmaxf(fmaxf(t5[3], t5[4]), sacc[kb][15]));
+            }
+            float mx = NKB == 1 ? bm[0] : fmaxf(bm[0], bm[NKB - 1]);
             mx = half_max(mx);
             // Rescale O and l only when some row max of this wave grew (a
             // wave-uniform branch); the offset is always the exact running max.
@@ -405,17 +448,19 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                 const float m_new = fmaxf(m_use, mx);
                 const float alpha = fast_exp2((m_use - m_new) * p.scale_log2);  // 0 on the first tile
                 m_use = m_new;
-                lsum[0] *= alpha;
-                lsum[1] *= alpha;
+                if (kt > 0) {   // tile 0 is every wave's first: O and l are still zero
+                    lsum[0] *= alpha;
+                    lsum[1] *= alpha;
 #pragma unroll
-                for (int db = 0; db < NDB; ++db)
+                    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+                        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+                }
             }
             const float moff = (m_use == -INFINITY) ? 0.f : -m_use * p.scale_log2;
             uint32_t pk[2][8];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; r += 2) {
                     const float p0 = fast_exp2(__builtin_fmaf(sacc[kb][r], p.scale_log2, moff));
@@ -425,7 +470,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             // l sums the probabilities as rounded for the PV product, so O is
             // normalised by exactly the weights it was built from.
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const u32x2_t pair = {pk[kb][2 * c], pk[kb][2 * c + 1]};
@@ -433,7 +478,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                 }
             // ---- O^T += V^T P^T ----
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
                     u32x4_t bw = {pk[kb][4 * c], pk[kb][4 * c + 1], pk[kb][4 * c + 2], pk[kb][4 * c + 3]};
@@ -469,9 +514,31 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             constexpr int t = decltype(t_c)::value;
             if (t < nt) swrite(t, t_c);
         });
+        if constexpr (BIAS) {
+            if (wave == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x4_t v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = (16 * hi + 4 * j + e <= col) ? 0.f : -INFINITY;
+                    dtab[64 * j + lane] = v;
+                }
+            }
+        }
         __syncthreads();
         // No barrier from here on: each wave runs its own tiles and leaves.
-        for (int kt = 0; kt < nt && wave_needs(kt); ++kt) compute_tile(kt, kt);
+        if constexpr (BIAS) {
+            if (wave_active) {
+                const int kdiag = q0w / BN;   // tile of the wave's diagonal block (kdiag < nt)
+                for (int kt = 0; kt < kdiag; ++kt) compute_tile(kt, kt, std::integral_constant<int, 1>{});
+                if (q0w % BN)
+                    compute_tile(kdiag, kdiag, std::integral_constant<int, 2>{});
+                else
+                    compute_tile(kdiag, kdiag, std::integral_constant<int, 3>{});
+            }
+        } else {
+            for (int kt = 0; kt < nt && wave_needs(kt); ++kt) compute_tile(kt, kt, std::integral_constant<int, 0>{});
+        }
     } else {
         gload(0, std::integral_constant<int, 0>{});
         swrite(0, std::integral_constant<int, 0>{});
@@ -489,7 +556,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             // number of loads in flight, and hence the vmcnt wait before the LDS
             // write below, is the same on every path.
             gload(min(kt + 2, nt - 1), set_c);
-            if (wave_needs(kt)) compute_tile(SET, kt);
+            if (wave_needs(kt)) compute_tile(SET, kt, std::integral_constant<int, 0>{});
             if (kt + 1 < nt) swrite(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
             __syncthreads();
         };
@@ -501,10 +568,41 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
 
     // ---- epilogue: normalise, store O, m, l ----
     const float l_sum = half_sum(lsum[0][0] + lsum[1][0]);   // relative to m_use
-    if (wave_active && qi < S) {
-        const float inv = 1.0f / l_sum;
-        // l of the output is relative to the exact row max
-        const float l_tot = l_sum * fast_exp2((m_use - m_true) * p.scale_log2);
+    // Streaming form: O goes out through LDS.  A lane holds 8-byte pieces of
+    // its row, and stores of those (16 bytes of each of 32 rows per
+    // instruction) write partial lines; each wave instead writes its 32 x D
+    // block to its own slice of the K/V stages (free: the loop ends on a
+    // barrier), 16-byte chunks XOR-swizzled by row, and stores whole rows,
+    // 64 / CPR rows per instruction (measured 5-16% faster at S 300-1,000,
+    // head_dim 64 and 128; no gain at 32, whose 64-byte rows the direct
+    // stores already fill in four instructions).  The resident form keeps the
+    // direct stores: its waves end at different times and a barrier before
+    // the stores cost more than it saved.
+    const float inv = 1.0f / l_sum;
+    if constexpr (NTR == 0 && D >= 64) {
+        static_assert(NST * 2 * BN >= NW * 32, "O staging must fit in the K/V stages");
+        T *ost = &smem[0][0][0] + wave * 32 * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int c = 4 * db + g4;   // 16-byte chunk of the row
+                u32x2_t w2 = {E::pack2(acc[db][4 * g4] * inv, acc[db][4 * g4 + 1] * inv),
+                              E::pack2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv)};
+                *(u32x2_t *)(ost + col * D + 8 * (c ^ (col % CPR)) + 4 * hi) = w2;
+            }
+        // LDS operations of one wave complete in order; this keeps the
+        // compiler from moving the reads above the other lanes' writes.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        constexpr int RPI = 64 / CPR;   // rows per store instruction
+        const int c = lane % CPR;
+#pragma unroll
+        for (int it = 0; it < 32 / RPI; ++it) {
+            const int r = it * RPI + lane / CPR;
+            const u32x4_t val = *(const u32x4_t *)(ost + r * D + 8 * (c ^ (r % CPR)));
+            if (wave_active && q0w + r < S) *(u32x4_t *)(og + (int64_t)(q0w + r) * p.o_ss + 8 * c) = val;
+        }
+    } else if (wave_active && qi < S) {
         T *orow = og + (int64_t)qi * p.o_ss;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
@@ -515,6 +613,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                               E::pack2(acc[db][4 * g4 + 2] * inv, acc[db][4 * g4 + 3] * inv)};
                 *(u32x2_t *)(orow + d) = w2;
             }
+    }
+    if (wave_active && qi < S) {
+        // l of the output is relative to the exact row max
+        const float l_tot = l_sum * fast_exp2((m_use - m_true) * p.scale_log2);
         if (hi == 0) {
             const int64_t mi = (int64_t)bh * S + qi;
             const float mval = m_true * p.scale;
