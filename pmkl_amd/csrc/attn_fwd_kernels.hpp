@@ -374,9 +374,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     // softmax, O update.  KIND 0: element-wise mask where the tile straddles
     // the diagonal or the end of the sequence; 1: no mask; 2: diagonal block
     // second (BIAS only); 3: diagonal block first, second block masked
-    // (BIAS only).
+    // (BIAS only).  + FIRST (BIAS only): the wave's first tile, whose row
+    // sums and O start from zero MFMA accumulators and need no rescale.
+    constexpr int FIRST = 4;
     auto compute_tile = [&](int st, int kt, auto kind_c) __attribute__((always_inline)) {
-        constexpr int KIND = decltype(kind_c)::value;
+        constexpr int KIND = decltype(kind_c)::value & 3;
+        constexpr bool IS_FIRST = (decltype(kind_c)::value & FIRST) != 0;
         constexpr int NKB = KIND == 3 ? 1 : 2;   // 32-key blocks computed
         const int kbase = kt * BN;
         {
@@ -444,7 +447,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
             // Rescale O and l only when some row max of this wave grew (a
             // wave-uniform branch); the offset is always the exact running max.
             m_true = fmaxf(m_true, mx);
-            if (__builtin_amdgcn_ballot_w64(mx > m_use + lazy_raw)) {
+            if (IS_FIRST) {
+                m_use = mx;   // finite: every row has a visible key in its first tile
+            } else if (__builtin_amdgcn_ballot_w64(mx > m_use + lazy_raw)) {
                 const float m_new = fmaxf(m_use, mx);
                 const float alpha = fast_exp2((m_use - m_new) * p.scale_log2);  // 0 on the first tile
                 m_use = m_new;
@@ -474,7 +479,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const u32x2_t pair = {pk[kb][2 * c], pk[kb][2 * c + 1]};
-                    lsum[c & 1] = E::sum4(pair, lsum[c & 1]);
+                    lsum[c & 1] = E::sum4(pair, (IS_FIRST && kb == 0 && c < 2) ? f32x4_t{0.f, 0.f, 0.f, 0.f} : lsum[c & 1]);
                 }
             // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -495,7 +500,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
                         s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)a1);
                         typedef short s16x8_t __attribute__((ext_vector_type(8)));
                         s16x8_t a8 = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-                        acc[db] = E::mma(__builtin_bit_cast(frag, a8), bfr, acc[db]);
+                        acc[db] = E::mma(__builtin_bit_cast(frag, a8), bfr,
+                                         (IS_FIRST && kb == 0 && c == 0) ? f32x16_t{} : acc[db]);
                     }
                 }
         }
@@ -530,11 +536,19 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
         if constexpr (BIAS) {
             if (wave_active) {
                 const int kdiag = q0w / BN;   // tile of the wave's diagonal block (kdiag < nt)
-                for (int kt = 0; kt < kdiag; ++kt) compute_tile(kt, kt, std::integral_constant<int, 1>{});
-                if (q0w % BN)
-                    compute_tile(kdiag, kdiag, std::integral_constant<int, 2>{});
-                else
-                    compute_tile(kdiag, kdiag, std::integral_constant<int, 3>{});
+                if (kdiag == 0) {
+                    if (q0w % BN)
+                        compute_tile(0, 0, std::integral_constant<int, 2 | FIRST>{});
+                    else
+                        compute_tile(0, 0, std::integral_constant<int, 3 | FIRST>{});
+                } else {
+                    compute_tile(0, 0, std::integral_constant<int, 1 | FIRST>{});
+                    for (int kt = 1; kt < kdiag; ++kt) compute_tile(kt, kt, std::integral_constant<int, 1>{});
+                    if (q0w % BN)
+                        compute_tile(kdiag, kdiag, std::integral_constant<int, 2>{});
+                    else
+                        compute_tile(kdiag, kdiag, std::integral_constant<int, 3>{});
+                }
             }
         } else {
             for (int kt = 0; kt < nt && wave_needs(kt); ++kt) compute_tile(kt, kt, std::integral_constant<int, 0>{});
@@ -578,7 +592,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     // stores already fill in four instructions).  The resident form keeps the
     // direct stores: its waves end at different times and a barrier before
     // the stores cost more than it saved.
-    const float inv = 1.0f / l_sum;
+    const float inv = __builtin_amdgcn_rcpf(l_sum);   // v_rcp_f32 (1 ulp); not stored where l_sum is 0
     if constexpr (NTR == 0 && D >= 64) {
         static_assert(NST * 2 * BN >= NW * 32, "O staging must fit in the K/V stages");
         T *ost = &smem[0][0][0] + wave * 32 * D;
