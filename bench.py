@@ -99,29 +99,35 @@ def read_traffic(config: str, kernel: str, name: str | None = None):
     return float(m.group(1)) if m else None
 
 
-def read_profile(config: str, kernel: str, flops: float, peak: float):
+def read_profile(config: str, kernel: str, work: float, peak: float, unit_scale: float = 1e12):
     """The committed kernel traces of `kernel` at `config`
-    (profiles/attn_fwd_w64_<config>_kernel_trace.txt): one "lease:" line per
-    fresh GPU lease with the trace mean of the timed dispatches (us) and the
+    (profiles/<family>_<config>_kernel_trace.txt, family = the kernel's name
+    without "_kernel<...>", e.g. attn_fwd_w64): one "lease:" line per fresh
+    GPU lease with the trace mean of the timed dispatches (us) and the
     shader clock of that lease; returns them with the fraction of peak they
-    give, or None when no summary was taken on this kernel."""
-    path = ROOT / "profiles" / f"attn_fwd_w64_{config}_kernel_trace.txt"
+    give (work per launch / trace mean / unit_scale / peak: FLOP and 1e12 for
+    TFLOP/s, bytes and 1e9 for GB/s), or None when no summary was taken on
+    this kernel."""
+    family = kernel.split("<")[0].removesuffix("_kernel")
+    path = ROOT / "profiles" / f"{family}_{config}_kernel_trace.txt"
     if not path.exists():
         return None
     txt = path.read_text()
     k = re.search(r"^kernel_id:\s*(.+?)\s*$", txt, re.M)
     if k is None or k.group(1) != kernel.split(" grid")[0]:
         return None
-    leases = [{"lease": m.group(1), "trace_mean_us": float(m.group(2)), "shader_clock_GHz": float(m.group(3))}
-              for m in re.finditer(r"^lease:\s*(\S+)\s+trace_mean_us\s+([0-9.]+)\s+shader_clock_GHz\s+([0-9.]+)",
+    # shader_clock_GHz is "n/a" where the counter window cannot give a clock (kernels of a few us).
+    leases = [{"lease": m.group(1), "trace_mean_us": float(m.group(2)),
+               "shader_clock_GHz": None if m.group(3) == "n/a" else float(m.group(3))}
+              for m in re.finditer(r"^lease:\s*(\S+)\s+trace_mean_us\s+([0-9.]+)\s+shader_clock_GHz\s+([0-9.]+|n/a)",
                                    txt, re.M)]
     if not leases:
         return None
     best = min(x["trace_mean_us"] for x in leases)
     mean = sum(x["trace_mean_us"] for x in leases) / len(leases)
     return {"file": str(path.relative_to(ROOT)), "leases": leases,
-            "frac_best_lease": round(flops / (best / 1e6) / 1e12 / peak, 4),
-            "frac_mean_of_leases": round(flops / (mean / 1e6) / 1e12 / peak, 4)}
+            "frac_best_lease": round(work / (best / 1e6) / unit_scale / peak, 4),
+            "frac_mean_of_leases": round(work / (mean / 1e6) / unit_scale / peak, 4)}
 
 
 def _host_cpu():
@@ -582,6 +588,9 @@ def main():
     value = flops * args.steps / elapsed_s / 1e12
     achieved = flops / (avg_launch_ms / 1e3) / 1e12
     peak = PEAK_TFLOPS[w.dtype]
+    # The bound of the roofline: HBM where the arithmetic intensity times the
+    # HBM peak is below the MFMA peak (C5), else the matrix cores.
+    hbm_bound = flops / alg_bytes * PEAK_HBM_GBS / 1e3 < peak
     kernel = capi.attn_fwd_kernel_name(cargs)
     traffic = read_traffic(w.name, kernel)
 
@@ -606,16 +615,22 @@ def main():
                    "flops_per_step": flops, "flop_count": "2*B*H*D*S*(S+1)",
                    "alg_bytes_per_step": alg_bytes, "parallelism": "single GPU"},
         "pct_of_mfma_peak": round(100.0 * value / peak, 2),
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": traffic,
+        "roofline": {**({"bound": "hbm", "achieved": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9, 1),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)} if hbm_bound else
+                        {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                         "frac": round(achieved / peak, 4)}),
+                     "traffic": traffic,
                      "kernel": kernel,
                      "avg_launch_us": round(avg_launch_ms * 1e3, 2),
                      "launches": {"n": len(per_launch_us),
                                   "median_us": round(per_launch_us[len(per_launch_us) // 2], 2),
                                   "min_us": round(per_launch_us[0], 2), "max_us": round(per_launch_us[-1], 2),
-                                  "frac_at_median": round(flops / (per_launch_us[len(per_launch_us) // 2] / 1e6)
-                                                          / 1e12 / peak, 4)},
-                     "profile": read_profile(w.name, kernel, flops, peak),
+                                  "frac_at_median": round((alg_bytes / 1e9 / PEAK_HBM_GBS if hbm_bound else
+                                                           flops / 1e12 / peak)
+                                                          / (per_launch_us[len(per_launch_us) // 2] / 1e6), 4)},
+                     "profile": (read_profile(w.name, kernel, alg_bytes, PEAK_HBM_GBS, 1e9) if hbm_bound else
+                                 read_profile(w.name, kernel, flops, peak)),
                      "hbm_GBs_algorithmic": round(alg_bytes / (avg_launch_ms / 1e3) / 1e9, 1)},
         "cpu_baseline": cpu,
         "torch_sdpa": sdpa,
