@@ -20,7 +20,9 @@
 //    MFMA operand reads are bank-conflict free; Q stays in VGPRs.
 //  * Key tiles wholly above the diagonal are never loaded or computed; the
 //    mask is applied element-wise only on tiles that straddle the diagonal or
-//    the end of the sequence.  Workgroups are issued longest-first.
+//    the end of the sequence (in the causal resident form at head_dim 32 it
+//    is the accumulator input of the diagonal block's score MFMA instead).
+//    Workgroups are issued longest-first.
 //  * Softmax is FA2-style: running max and per-lane partial sum, exp2 with
 //    scale*log2(e) folded into one FMA, normalisation once in the epilogue.
 #pragma once
