@@ -803,7 +803,12 @@ void attn_fwd_w64_kernel(AttnParams p) {
             sm_mask(0, S0{});
 #pragma unroll
             for (int k = 0; k < Sch::NMU; ++k) max_unit(S0{}, k);
-            apply_rescale();
+            // Tile 0 always passes the rescale test (m_use was -inf), but O
+            // and the row sums were just zeroed: nothing to scale (the
+            // multiply by alpha = 0 cost ~200 vector instructions per wave
+            // and item, AGPR reads and writes included).
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) rescale[qb] = false;
         }
         // No barrier here with a barrier per position: iteration 0 refills
         // slots 3 and 2 (K(3), V(2)), free since the previous item's last
