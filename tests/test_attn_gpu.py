@@ -79,7 +79,10 @@ def test_small_shapes_vs_oracle(device, dtype, D, causal):
 # kernel in its resident form, head_dim 128 at S 300 (few work items) its
 # 4-wave streaming form; head_dim 128 from S 385 and causal head_dim 64 from
 # S 512 run the 64-row kernel, whose epilogue has its own float m/l store.
-ML_F32_SHAPES = [(200, 64, True), (300, 128, True), (520, 128, True), (520, 128, False), (1024, 64, True)]
+ML_F32_SHAPES = [(200, 64, True), (300, 128, True), (520, 128, True), (520, 128, False), (1024, 64, True),
+                 # head_dim 32 causal resident form (diagonal mask as the MFMA accumulator
+                 # input, zero-start first tile), and the streaming form's LDS-staged O
+                 (200, 32, True), (256, 32, True), (600, 64, False)]
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
@@ -332,6 +335,37 @@ def test_running_max_grows_every_tile(device, dtype, slope, causal):
     o, m, l = _run_capi(q, k, v, device, causal=causal)
     rows = _sample_rows(S, 24, seed=int(slope * 10) + causal)
     errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)
+    _say(f"{tag}: {errs}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("S,D,causal", [(256, 32, True), (200, 32, True), (256, 64, True), (600, 64, False)])
+def test_running_max_grows_short(device, dtype, S, D, causal):
+    """Rising scores as in test_running_max_grows_every_tile (slope 2: the
+    running max passes the lazy-rescale threshold on every key tile) on the
+    8-wave kernel: its resident form at head_dim 32 and 64, where every tile
+    after a wave's first rescales O and l, and its streaming form (S 600,
+    non-causal head_dim 64), every row against the oracle."""
+    import torch
+
+    from pmkl_amd.workloads import torch_dtype
+    from tests.parity import check_outputs
+
+    B, H = 2, 3
+    tag = f"{dtype} rising scores B{B} H{H} S{S} D{D} causal={causal}"
+    _say(f"case {tag}")
+    g = torch.Generator().manual_seed(93 + S + D)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    a = (2.0 * D ** 0.5) ** 0.5
+    j = torch.arange(S, dtype=torch.float32)
+    q = a * u.expand(B, H, S, D) + 0.3 * torch.randn(B, H, S, D, generator=g)
+    k = (a * j[:, None]) * u
+    k = k.expand(B, H, S, D) + 0.3 * torch.randn(B, H, S, D, generator=g)
+    v = torch.randn(B, H, S, D, generator=g)
+    q, k, v = (x.to(torch_dtype(dtype)) for x in (q, k, v))
+    o, m, l = _run_capi(q, k, v, device, causal=causal)
+    errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, label=tag)
     _say(f"{tag}: {errs}")
 
 
