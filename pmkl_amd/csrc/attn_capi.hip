@@ -592,6 +592,7 @@ int plan_fwd(const pmkl_attn_fwd_args *a, FwdPlan *pl) {
     // Reference scale: 1.0f / std::sqrt((float)hidden_size), fused_self_attention.cpp:30.
     p.scale = a->scale > 0.f ? a->scale : 1.0f / std::sqrt((float)D);
     p.scale_log2 = p.scale * 1.4426950408889634f;
+    p.lazy_raw = pmkl_amd::kLazyLog2 / p.scale_log2;   // IEEE float division, as the kernels' was
     p.ml_f32 = a->ml_dtype == PMKL_DTYPE_F32 ? 1 : 0;
     // XCD-grouped issue order needs whole head pairs (causal) or heads per XCD.
     p.xcd_order = (a->dtype != PMKL_DTYPE_F32 && xcd_order_enabled() && (B * H) % (a->is_causal ? 16 : 8) == 0) ? 1 : 0;

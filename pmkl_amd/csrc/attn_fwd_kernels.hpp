@@ -66,6 +66,8 @@ struct AttnParams {
     float scale_log2;    // scale * log2(e)
     int32_t ml_f32;      // 1: m/l stored as float, 0: stored in the tensor dtype
     int32_t xcd_order;   // 1: workgroup index read as (XCD, head group, q-tile), see map_workgroup
+    float lazy_raw;      // kLazyLog2 / scale_log2: the 16-bit kernels' rescale threshold in raw
+                         // dot-product units (divided once on the host, not per wave)
 };
 
 constexpr int kWaves = 4;                // waves per workgroup of the fp32 kernel
@@ -349,7 +351,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     // MFMAs (sum4) into component 0 .. 3 alike; two accumulators alternate so
     // that consecutive row-sum MFMAs do not wait on each other.
     f32x4_t lsum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    const float lazy_raw = kLazyLog2 / p.scale_log2;
+    const float lazy_raw = p.lazy_raw;
 
     // Per-lane constant parts of the LDS addresses.
     const int arow = key_of_arow(col);        // K tile row read by this lane (per 32-key block)

@@ -468,7 +468,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
     // SGPRs by VALU moves right before each MFMA that reads it (the MFMAs
     // are inline asm, so the compiler inserts no wait states for them).
     asm volatile("" : "+v"(ones));
-    const float lazy_raw = kLazyLog2 / p.scale_log2;
+    const float lazy_raw = p.lazy_raw;
     auto reset_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
