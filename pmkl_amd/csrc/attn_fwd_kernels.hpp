@@ -369,8 +369,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_fwd_mfma16_kernel(AttnPa
     // is skipped.  The mask lives in LDS (dtab[j][lane] = registers 4j ..
     // 4j+3 of lane; wave 0 writes it before the workgroup's barrier), read
     // with four conflict-free 16-byte reads: kept in VGPRs it is rebuilt by
-    // the compiler on every use.  Only at head_dim 32: the extra registers
-    // of the three tile bodies would cost waves per SIMD at 64 and 128.
+    // the compiler on every use.  Only at head_dim 32 (107 VGPRs, four waves
+    // per SIMD): with the five tile bodies of this form (KIND 1-3, FIRST or
+    // not) the head_dim-64 kernel needs 159, three waves per SIMD.
     constexpr bool BIAS = CAUSAL && NTR > 0 && D == 32;
     __shared__ __attribute__((aligned(16))) f32x4_t dtab[BIAS ? 4 * 64 : 1];
 
