@@ -99,3 +99,48 @@ def test_random_shape_forward_many_heads(device, case):
     fixed = [0, 1, 63, 64, 127, 128, 255, 256, S // 2, S - 65, S - 64, S - 1]
     rows = sorted(set(r for r in fixed + rng.choice(S, size=8, replace=False).tolist() if 0 <= r < S))
     _say(f"  {check_outputs(q, k, v, o, m, l, dtype, causal=causal, rows=rows, label=tag)}")
+
+
+N_SHORT = 120
+
+
+def _short_cases(seed=20261204, n=N_SHORT):
+    """Short sequences (S 1-300) at head_dim 32 and 64 in the 16-bit dtypes,
+    mostly causal, with float m/l on some: the 8-wave kernel's resident form
+    (diagonal mask as the score MFMA's accumulator input at head_dim 32, every
+    row-block pairing) and its streaming form just above it."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    out = []
+    for i in range(n):
+        out.append(dict(B=int(rng.integers(1, 4)), H=int(rng.integers(1, 7)), S=int(rng.integers(1, 301)),
+                        D=int(rng.choice([32, 32, 64])), dtype=str(rng.choice(["bf16", "fp16"])),
+                        causal=bool(rng.random() < 0.75), ml32=bool(rng.random() < 0.25), seed=7400 + i))
+    return out
+
+
+def test_random_short_sequences_forward(device):
+    """Forward only, every row of every case against the float64 oracle; the
+    cases run in one test (each is a few milliseconds) and each is named
+    before it runs."""
+    import torch
+
+    import pmkl_amd
+    from pmkl_amd.workloads import small_inputs
+    from tests.parity import check_outputs
+    from tests.test_attn_bwd_gpu import _say
+
+    worst = 0.0
+    for case in _short_cases():
+        B, H, S, D, dtype, causal, ml32 = (case[k] for k in ("B", "H", "S", "D", "dtype", "causal", "ml32"))
+        tag = f"random short B{B} H{H} S{S} D{D} {dtype} causal={causal} ml_f32={ml32} seed={case['seed']}"
+        _say(f"case {tag}")
+        q, k, v = small_inputs(B, H, S, D, dtype, seed=case["seed"])
+        o, m, l = pmkl_amd.attn_fwd(q.to("cuda:0"), k.to("cuda:0"), v.to("cuda:0"), is_causal=causal,
+                                    ml_dtype=torch.float32 if ml32 else None)
+        torch.cuda.synchronize()
+        if ml32:
+            assert m.dtype == torch.float32 and l.dtype == torch.float32
+            m, l = m.to(q.dtype), l.to(q.dtype)
+        errs = check_outputs(q, k, v, o, m, l, dtype, causal=causal, label=tag, check_ml=not ml32)
+        worst = max(worst, errs["worst_over_bound"])
+    _say(f"{len(_short_cases())} short cases, worst O error / bound {worst:.3f}")
