@@ -58,13 +58,17 @@
 
 namespace pmkl_amd {
 
-// One LDS-DMA of 16 bytes per lane: bytes [off, off+16) of buffer r land at
-// LDS byte address m0 + 16 * lane.  Inline asm, so the compiler neither waits
-// for it before unrelated LDS reads nor counts it; the kernel waits itself.
-// An SALU write of M0 needs one wait state before an LDS-DMA reads it.
-__device__ __forceinline__ void w64_lds_dma16(__amdgpu_buffer_rsrc_t r, int off, unsigned m0) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0),
-                 "s"(r)
+// One LDS-DMA of 16 bytes per lane: bytes [off + so, off + so + 16) of
+// buffer r (off per lane, so wave-uniform) land at LDS byte address
+// lds + LOFF + 16 * lane.  Inline asm, so the compiler neither waits for it
+// before unrelated LDS reads nor counts it; the kernel waits itself.  M0 is
+// formed here from the wave's LDS base and the compile-time slot offset (so
+// the compiler does not keep one SGPR per slot).  An SALU write of M0 needs
+// one wait state before an LDS-DMA reads it.
+template <int LOFF>
+__device__ __forceinline__ void w64_lds_dma16(__amdgpu_buffer_rsrc_t r, int off, int so, unsigned lds) {
+    asm volatile("s_add_u32 m0, %1, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds" ::"v"(off), "s"(lds),
+                 "s"(r), "s"(so), "n"(LOFF)
                  : "memory");
 }
 
@@ -399,30 +403,79 @@ void attn_fwd_w64_kernel(AttnParams p) {
     const int k_tile_bytes = (int)(BN * p.k_ss * sizeof(T));
     const int v_tile_bytes = (int)(BN * p.v_ss * sizeof(T));
     const unsigned lds_w = lds0 + (unsigned)(wave * 1024);
-    // DMA j of the K / V tile at stream position kt of the current item into
-    // LDS slot sl (= kt % NSL, passed by the caller).  Positions past the
-    // item's own (npos) are the next item's tiles 0, 1, 2; tiles are clamped
-    // to the item's last one (the copies past it are never read).
-    auto dma_k = [&](int kt, int sl, int j) __attribute__((always_inline)) {
-        const bool nx = has_next && kt >= npos;
-        const T *base = nx ? kg_n : kg;
-        const int tile = nx ? min(kt - npos, nt_n - 1) : min(kt, nt - 1);
-        w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, k_records, 0x00020000),
-                      koff[j] + tile * k_tile_bytes, lds_w + (unsigned)(sl * TILE_BYTES + j * 16 * NT));
+    // The K and V streams run one tile per stream position: position kt of
+    // an item is its tile min(kt, nt - 1) (copies past the last tile are never
+    // read), and positions npos, npos + 1, ... are the next item's tiles 0, 1,
+    // ...  Each stream keeps its source as it goes: the buffer resource of the
+    // head its next tile comes from, the tile's byte offset (the DMAs'
+    // soffset) and the offset of that head's last tile of the item.  A stream
+    // moves to the next item's head after its DMAs of position npos - 1
+    // (sw_at = npos with a next item; never without).
+    __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(nullptr, (short)0, 0, 0x00020000);
+    __amdgpu_buffer_rsrc_t vrs = krs;
+    int kso = 0, vso = 0, klast = 0, vlast = 0, sw_at = -1;
+    auto stream_start = [&]() __attribute__((always_inline)) {
+        krs = __builtin_amdgcn_make_buffer_rsrc((void *)kg, (short)0, k_records, 0x00020000);
+        vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vg, (short)0, v_records, 0x00020000);
+        kso = vso = 0;
+        klast = (nt - 1) * k_tile_bytes;
+        vlast = (nt - 1) * v_tile_bytes;
     };
-    auto dma_v = [&](int kt, int sl, int j) __attribute__((always_inline)) {
-        const bool nx = has_next && kt >= npos;
-        const T *base = nx ? vg_n : vg;
-        const int tile = nx ? min(kt - npos, nt_n - 1) : min(kt, nt - 1);
-        w64_lds_dma16(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, v_records, 0x00020000),
-                      voff[j] + tile * v_tile_bytes, lds_w + (unsigned)((NSL + sl) * TILE_BYTES + j * 16 * NT));
+    // after the K (V) DMAs of position kt: move on to position kt + 1
+    auto next_k = [&](int kt, bool may_switch) __attribute__((always_inline)) {
+        if (may_switch && __builtin_expect(kt + 1 == sw_at, 0)) {
+            krs = __builtin_amdgcn_make_buffer_rsrc((void *)kg_n, (short)0, k_records, 0x00020000);
+            kso = 0;
+            klast = (nt_n - 1) * k_tile_bytes;
+        } else {
+            kso = min(kso + k_tile_bytes, klast);
+        }
     };
-    // DMA i of iteration t: K(t+3) into slot (t+3) % NSL (slk), then V(t+2)
+    auto next_v = [&](int kt, bool may_switch) __attribute__((always_inline)) {
+        if (may_switch && __builtin_expect(kt + 1 == sw_at, 0)) {
+            vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vg_n, (short)0, v_records, 0x00020000);
+            vso = 0;
+            vlast = (nt_n - 1) * v_tile_bytes;
+        } else {
+            vso = min(vso + v_tile_bytes, vlast);
+        }
+    };
+    // DMA j of the stream's current tile into LDS slot SL (= kt % NSL).
+    auto dma_k = [&](auto sl_c, auto j_c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(sl_c)::value, J = decltype(j_c)::value;
+        w64_lds_dma16<SL * TILE_BYTES + J * 16 * NT>(krs, koff[J], kso, lds_w);
+    };
+    auto dma_v = [&](auto sl_c, auto j_c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(sl_c)::value, J = decltype(j_c)::value;
+        w64_lds_dma16<(NSL + SL) * TILE_BYTES + J * 16 * NT>(vrs, voff[J], vso, lds_w);
+    };
+    // DMA i of position t: K(t+3) into slot (t+3) % NSL (slk), then V(t+2)
     // into slot (t+2) % NSL (slv).  The slots hold K(t-1) and V(t-2), last
-    // read before the previous iteration's barrier.
-    auto dma_step = [&](int t, int slk, int slv, int i) __attribute__((always_inline)) {
-        if (i < LOADS) dma_k(t + 3, slk, i);
-        else dma_v(t + 2, slv, i - LOADS);
+    // read before the previous position's barrier.  npos is a multiple of
+    // NSL, so the K stream can only switch at positions t = 0 (mod NSL) and
+    // the V stream at t = 1 (mod NSL): PH (t mod NSL, or -1 when not known at
+    // compile time) skips the test elsewhere.
+    // Slots as compile-time constants: SLK = (t + 3) % NSL, SLV = (t + 2) % NSL.
+    auto dma_step_c = [&](int t, auto slk_c, auto slv_c, auto i_c, auto ph_c) __attribute__((always_inline)) {
+        constexpr int PH = decltype(ph_c)::value, I = decltype(i_c)::value;
+        if constexpr (I < LOADS) {
+            dma_k(slk_c, std::integral_constant<int, I>{});
+            if constexpr (I == LOADS - 1) next_k(t + 3, PH < 0 || PH == 0);
+        } else {
+            dma_v(slv_c, std::integral_constant<int, I - LOADS>{});
+            if constexpr (I == 2 * LOADS - 1) next_v(t + 2, PH < 0 || PH == 1);
+        }
+    };
+    // All DMAs of position t, the slots known at run time only (t mod NSL).
+    auto dma_position = [&](int t) __attribute__((always_inline)) {
+        w64_static_for<0, NSL>([&](auto ph_c) __attribute__((always_inline)) {
+            constexpr int PH = decltype(ph_c)::value;
+            if ((t & (NSL - 1)) == PH)
+                w64_static_for<0, 2 * LOADS>([&](auto i_c) __attribute__((always_inline)) {
+                    dma_step_c(t, std::integral_constant<int, (PH + 3) % NSL>{},
+                               std::integral_constant<int, (PH + 2) % NSL>{}, i_c, std::integral_constant<int, -1>{});
+                });
+        });
     };
     // Barrier placement.  Head_dim 128 (and 32): one barrier per stream
     // position, at BARS, waiting until only the position's own DMAs (2 LOADS,
@@ -678,7 +731,9 @@ void attn_fwd_w64_kernel(AttnParams p) {
             }
             w64_static_for<0, 2 * LOADS>([&](auto j_c) __attribute__((always_inline)) {
                 constexpr int j = decltype(j_c)::value;
-                if constexpr ((PAIR ? j + 1 : Sch::dma_slot(j, 2 * LOADS)) == s) dma_step(t, SL3, SL2, j);
+                if constexpr ((PAIR ? j + 1 : Sch::dma_slot(j, 2 * LOADS)) == s)
+                    dma_step_c(t, std::integral_constant<int, SL3>{}, std::integral_constant<int, SL2>{}, j_c,
+                               std::integral_constant<int, PH>{});
             });
             if constexpr (s == Sch::MS0) {
                 w64_mfma_drain();   // the QK MFMAs of tile t+1 have written the scores
@@ -756,18 +811,22 @@ void attn_fwd_w64_kernel(AttnParams p) {
     set_item(item_index(0));
     set_next(item_index(1));
     load_q();
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        dma_k(0, 0, j);
-        dma_v(0, 0, j);
-    }
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) dma_k(1, 1, j);
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        dma_k(2, 2, j);
-        dma_v(1, 1, j);
-    }
+    stream_start();
+    sw_at = has_next ? npos : -1;
+    // K(0), V(0), K(1), K(2), V(1) (npos >= NSL = 4: no stream switches here)
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    w64_static_for<0, LOADS>([&](auto j_c) __attribute__((always_inline)) { dma_k(C0{}, j_c); });
+    next_k(0, false);
+    w64_static_for<0, LOADS>([&](auto j_c) __attribute__((always_inline)) { dma_v(C0{}, j_c); });
+    next_v(0, false);
+    w64_static_for<0, LOADS>([&](auto j_c) __attribute__((always_inline)) { dma_k(C1{}, j_c); });
+    next_k(1, false);
+    w64_static_for<0, LOADS>([&](auto j_c) __attribute__((always_inline)) { dma_k(C2{}, j_c); });
+    next_k(2, false);
+    w64_static_for<0, LOADS>([&](auto j_c) __attribute__((always_inline)) { dma_v(C1{}, j_c); });
+    next_v(1, false);
     sync_tiles();
 
     // Outputs of the previous item (its O, row sums and maxima stay in acc,
@@ -847,8 +906,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
         if (q_early) load_q_of(bh_nx, q0w_nx);
         // ---- remaining positions of the item: DMAs and barriers only ----
         for (; t < npos; ++t) {
-#pragma unroll
-            for (int i = 0; i < 2 * LOADS; ++i) dma_step(t, (t + 3) % NSL, (t + 2) % NSL, i);
+            dma_position(t);
             if (!PAIR || (t & 1)) sync_tiles();
         }
         w64_mfma_drain();   // the last PV MFMAs have written O
@@ -864,6 +922,7 @@ void attn_fwd_w64_kernel(AttnParams p) {
             ++r;
             set_item(item_index(r));
             set_next(item_index(r + 1));
+            sw_at = has_next ? npos : -1;
             if (!q_early) load_q();
         }
         if (!more) {
