@@ -616,15 +616,23 @@ void attn_fwd_w64_kernel(AttnParams p) {
             const int qb = k >> 2, kb = (k >> 1) & 1, r0 = 8 * (k & 1);
             const auto &sv = sc[SET][qb][kb];
             float m;
+            // Each unit is one asm block: the compiler puts a wait state after
+            // every inline-asm VALU instruction whose result the next one
+            // reads (it cannot rule out a transcendental), so a chain of
+            // separate statements would carry one s_nop per step.
             if ((k & 3) == 0) {   // first unit of the block: 8 values, 4 instructions
-                m = w64_max3(sv[r0], sv[r0 + 1], sv[r0 + 2]);
-                m = w64_max3(m, sv[r0 + 3], sv[r0 + 4]);
-                m = w64_max3(m, sv[r0 + 5], sv[r0 + 6]);
-                m = w64_max(m, sv[r0 + 7]);
+                asm("v_max3_f32 %0, %1, %2, %3\n\tv_max3_f32 %0, %0, %4, %5\n\t"
+                    "v_max3_f32 %0, %0, %6, %7\n\tv_max_f32 %0, %0, %8"
+                    : "=&v"(m)
+                    : "v"(sv[r0]), "v"(sv[r0 + 1]), "v"(sv[r0 + 2]), "v"(sv[r0 + 3]), "v"(sv[r0 + 4]),
+                      "v"(sv[r0 + 5]), "v"(sv[r0 + 6]), "v"(sv[r0 + 7]));
             } else {
                 m = mx[qb];
-#pragma unroll
-                for (int r = 0; r < 8; r += 2) m = w64_max3(m, sv[r0 + r], sv[r0 + r + 1]);
+                asm("v_max3_f32 %0, %0, %1, %2\n\tv_max3_f32 %0, %0, %3, %4\n\t"
+                    "v_max3_f32 %0, %0, %5, %6\n\tv_max3_f32 %0, %0, %7, %8"
+                    : "+v"(m)
+                    : "v"(sv[r0]), "v"(sv[r0 + 1]), "v"(sv[r0 + 2]), "v"(sv[r0 + 3]), "v"(sv[r0 + 4]),
+                      "v"(sv[r0 + 5]), "v"(sv[r0 + 6]), "v"(sv[r0 + 7]));
             }
             asm volatile("" : "+v"(m));
             mx[qb] = m;
