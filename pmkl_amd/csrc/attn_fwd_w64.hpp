@@ -64,12 +64,15 @@ namespace pmkl_amd {
 // before unrelated LDS reads nor counts it; the kernel waits itself.  M0 is
 // formed here from the wave's LDS base and the compile-time slot offset (so
 // the compiler does not keep one SGPR per slot).  An SALU write of M0 needs
-// one wait state before an LDS-DMA reads it.
+// one wait state before an LDS-DMA reads it.  The add writes SCC as well as
+// M0, and both are declared clobbered: the compiler must not keep a
+// comparison result in SCC across a DMA (it did, once code was added around
+// the loop, and a flag tested before a DMA and used after it read as 0).
 template <int LOFF>
 __device__ __forceinline__ void w64_lds_dma16(__amdgpu_buffer_rsrc_t r, int off, int so, unsigned lds) {
     asm volatile("s_add_u32 m0, %1, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds" ::"v"(off), "s"(lds),
                  "s"(r), "s"(so), "n"(LOFF)
-                 : "memory");
+                 : "memory", "scc", "m0");
 }
 
 // MFMAs with operands pinned to register files:
