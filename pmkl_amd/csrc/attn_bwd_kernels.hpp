@@ -492,6 +492,17 @@ __device__ __forceinline__ void bwd_static_for(F &&f) {
     }
 }
 
+// Causal mask of a dK/dV tile as one threshold per lane: query
+// qbase + 32 qb + 16 hi + r is visible to the lane's key kj iff
+// 32 qb + r >= kj - qbase - 16 hi, one compare against a constant per score.
+// Tiles wholly at or past the wave's last key get a threshold every register
+// passes.  Queries past S need no mask: their lse2 is +inf and their Q and
+// dout rows read as zero, so P = exp2(0 * c - inf) = 0 and dS = 0 exactly.
+template <bool CAUSAL>
+__device__ __forceinline__ int bwd_dkdv_mlim(int qbase, int k0w, int kj, int hi) {
+    return CAUSAL && qbase < k0w + 31 ? kj - qbase - 16 * hi : -64;
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_kernel(BwdParams p) {
     using E = Elt16<T>;
@@ -641,8 +652,9 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
                     const int m = n - 2 * NSQ, qb = m / NGQ, j = m % NGQ;
                     return bwd_tr_frag<T, D>((j & 1) ? Qv : Ov, qb, j / (2 * NDB), (j >> 1) % NDB, vrow0, vcol0);
                 };
-                // register r of block qb holds query qbase + 32 qb + 16 hi + r
-                const bool need_mask = (CAUSAL && qbase < k0w + 31) || (qbase + BN > S);
+                // register r of block qb holds query qbase + 32 qb + 16 hi + r;
+                // the causal mask keeps it iff 32 qb + r >= mlim (bwd_dkdv_mlim)
+                const int mlim = bwd_dkdv_mlim<CAUSAL>(qbase, k0w, kj, hi);
                 f32x16_t s[2], dp[2];
                 uint32_t pp[2][8], dsp[2][8];
                 f32x4_t l4[2][4], d4[2][4];
@@ -656,13 +668,11 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
                 };
                 // P and dS of registers 2u, 2u + 1 of block qb
                 auto unit = [&](int qb, int u) __attribute__((always_inline)) {
-                    const int rb = 32 * qb + 16 * hi, r = 2 * u;
+                    const int r = 2 * u;
                     float pv[2], dsv[2];
     #pragma unroll
                     for (int e = 0; e < 2; ++e) {
-                        const int q = qbase + rb + r + e;
-                        const bool vis = !need_mask || (q < S && (!CAUSAL || q >= kj));
-                        const float sv = vis ? s[qb][r + e] : -INFINITY;
+                        const float sv = !CAUSAL || 32 * qb + r + e >= mlim ? s[qb][r + e] : -INFINITY;
                         pv[e] = fast_exp2(__builtin_fmaf(sv, c, -l4[qb][(r + e) >> 2][(r + e) & 3]));
                         dsv[e] = pv[e] * (dp[qb][r + e] - d4[qb][(r + e) >> 2][(r + e) & 3]);
                     }
@@ -730,8 +740,9 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
                         if (m + RING < NSD) ring[m % RING] = sd_frag(m + RING);
                     }
                 }
-                // register r of block qb holds query qbase + 32 qb + 16 hi + r
-                const bool need_mask = (CAUSAL && qbase < k0w + 31) || (qbase + BN > S);
+                // register r of block qb holds query qbase + 32 qb + 16 hi + r;
+                // the causal mask keeps it iff 32 qb + r >= mlim (bwd_dkdv_mlim)
+                const int mlim = bwd_dkdv_mlim<CAUSAL>(qbase, k0w, kj, hi);
                 uint32_t pp[2][8], dsp[2][8];
     #pragma unroll
                 for (int qb = 0; qb < 2; ++qb) {
@@ -747,9 +758,7 @@ __global__ __launch_bounds__(bwd_waves_dkdv<D>() * 64, 1) void attn_bwd_dkdv_ker
                         float pv[2], dsv[2];
     #pragma unroll
                         for (int e = 0; e < 2; ++e) {
-                            const int q = qbase + rb + r + e;
-                            const bool vis = !need_mask || (q < S && (!CAUSAL || q >= kj));
-                            const float sv = vis ? s[qb][r + e] : -INFINITY;
+                            const float sv = !CAUSAL || 32 * qb + r + e >= mlim ? s[qb][r + e] : -INFINITY;
                             pv[e] = fast_exp2(__builtin_fmaf(sv, c, -l4[(r + e) >> 2][(r + e) & 3]));
                             dsv[e] = pv[e] * (dp[qb][r + e] - d4[(r + e) >> 2][(r + e) & 3]);
                         }
