@@ -305,8 +305,13 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
             const int st = kt % 3, st1 = (kt + 1) % 3;
             const int kbase = kt * BN;
             const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
-            if (wave_needed) {
-                const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+            // Two copies of the tile's work, with and without the mask (a
+            // wave masks only its last tile, and the one past S): written
+            // per score, the mask's compare and select cost ~130 scalar and
+            // vector instructions on every tile.
+            const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+            auto work = [&](auto mask_c) __attribute__((always_inline)) {
+                constexpr bool MASK = decltype(mask_c)::value;
                 const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
                 uint32_t dsk[2][8];
                 frag ring[RING];
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
 #pragma unroll
                         for (int e = 0; e < 2; ++e) {
                             const int key = kbase + 32 * kb + 16 * hi + r + e;
-                            const float sv = need_mask && key > lim ? -INFINITY : sc[kb][r + e];
+                            const float sv = MASK && key > lim ? -INFINITY : sc[kb][r + e];
                             pv[e] = fast_exp2(__builtin_fmaf(sv, c, -lse2));
                         }
                         if (PASS == 0) {
@@ -357,6 +362,10 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                         if (m + RING < NQ) qring[m % RING] = kt_frag(m + RING);
                     }
                 }
+            };
+            if (wave_needed) {
+                if (need_mask) work(std::true_type{});
+                else work(std::false_type{});
             }
             if (kt + 2 < nt) swrite((kt + 2) % 3);
             if (kt + 3 < nt) gload(kt + 3);
@@ -382,7 +391,10 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
             gload2(min(kt + 2, nt - 1), set_c);
             const int kbase = kt * BN;
             const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
-            if (wave_needed) {
+            // masked and unmasked copies, as in the pipelined loop
+            const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
+            auto work = [&](auto mask_c) __attribute__((always_inline)) {
+                constexpr bool MASK = decltype(mask_c)::value;
                 const T *Kk = smem[SET][0];
                 const T *Kv = smem[SET][1];
                 const T *Vk = smem[SET][2];
@@ -398,7 +410,6 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                     }
                 }
                 // register r of block kb holds key kbase + 32 kb + 16 hi + r
-                const bool need_mask = (CAUSAL && kbase + BN - 1 > q0w) || (kbase + BN > S);
                 const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
                 uint32_t dsk[2][8];
 #pragma unroll
@@ -409,7 +420,7 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
 #pragma unroll
                         for (int e = 0; e < 2; ++e) {
                             const int key = kbase + 32 * kb + 16 * hi + r + e;
-                            const float sv = need_mask && key > lim ? -INFINITY : s[kb][r + e];
+                            const float sv = MASK && key > lim ? -INFINITY : s[kb][r + e];
                             pv[e] = fast_exp2(__builtin_fmaf(sv, c, -lse2));
                         }
                         if (PASS == 0) {
@@ -432,6 +443,10 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                                 acc[db] = E::mma(bwd_tr_frag<T, D>(Kv, kb, cc, db, vrow0, vcol0), bfr, acc[db]);
                         }
                 }
+            };
+            if (wave_needed) {
+                if (need_mask) work(std::true_type{});
+                else work(std::false_type{});
             }
             if (kt + 1 < nt) swrite2(SET ^ 1, std::integral_constant<int, SET ^ 1>{});
             __syncthreads();
