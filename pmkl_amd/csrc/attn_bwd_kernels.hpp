@@ -128,6 +128,16 @@ __device__ __forceinline__ float bwd_load_ml(const void *base, int64_t i, bool f
     return f32 ? ((const float *)base)[i] : (float)((const T *)base)[i];
 }
 
+// 16 bytes per lane from a buffer straight into LDS at M0 + 16 lane, M0 =
+// lds + LOFF (the dQ pass's K/V staging).  The M0 write needs one wait state
+// before the load; s_add_u32 also writes SCC, so both are declared clobbered.
+template <int LOFF>
+__device__ __forceinline__ void bwd_lds_dma16(__amdgpu_buffer_rsrc_t r, int off, unsigned lds) {
+    asm volatile("s_add_u32 m0, %1, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(lds),
+                 "s"(r), "n"(LOFF)
+                 : "memory", "scc", "m0");
+}
+
 // ---------------------------------------------------------------------------
 // pass 1: dQ (and the row vectors D_n, log2-sum-exp)
 // ---------------------------------------------------------------------------
@@ -185,9 +195,43 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
     const float lse2 = m_i * 1.4426950408889634f + __log2f(l_i);
     const float c = p.scale_log2;
 
-    // ---- staging: tile kt lives in LDS stage kt % 3; the registers hold the
-    // tile two ahead of the one being computed ----
-    u32x4_t kreg[LOADS], vreg[LOADS];
+    // ---- staging of the pipelined loop by LDS DMA: tile kt lands in stage
+    // kt % 3, 16 bytes per lane straight from memory.  Lane `lane` of wave
+    // `wave` fills chunk slot j*THREADS + 64*wave + lane of each layout (LDS
+    // bytes layout_base + 16 THREADS j + 1024 wave + 16 lane) with the logical
+    // chunk that the layout's XOR swizzle places there. ----
+    constexpr int TILE_BYTES = BN * D * (int)sizeof(T);
+    int doffk[LOADS], doffkt[LOADS], doffv[LOADS];   // K rows, K transposed layout, V rows
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int sl = j * kBwdThreads + tid;
+        const int row = sl / CPR, pp = sl % CPR;
+        doffk[j] = (row * kss + 8 * (pp ^ swz_k<CPR>(row))) * (int)sizeof(T);
+        doffkt[j] = (row * kss + 8 * (pp ^ swz_v<CPR>(row))) * (int)sizeof(T);
+        doffv[j] = (row * vss + 8 * (pp ^ swz_k<CPR>(row))) * (int)sizeof(T);
+    }
+    const unsigned lds_w = (unsigned)(uintptr_t)(__attribute__((address_space(3))) T *)&smem[0][0][0] + 1024u * wave;
+    // All DMAs of tile kt into stage kt % 3 (rows past S read as zero).
+    auto dma_tile = [&](int kt) __attribute__((always_inline)) {
+        static_assert(!PIPE || !PARTIAL, "the DMA staging covers whole tiles");
+        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S, kss);
+        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S, vss);
+        const unsigned base = lds_w + (unsigned)((kt % 3) * 3 * TILE_BYTES);
+        bwd_static_for<0, LOADS>([&](auto j_c) __attribute__((always_inline)) {
+            constexpr int J = decltype(j_c)::value;
+            bwd_lds_dma16<0 * TILE_BYTES + 16 * kBwdThreads * J>(kr, doffk[J], base);
+            bwd_lds_dma16<1 * TILE_BYTES + 16 * kBwdThreads * J>(kr, doffkt[J], base);
+            bwd_lds_dma16<2 * TILE_BYTES + 16 * kBwdThreads * J>(vr, doffv[J], base);
+        });
+    };
+    // The DMAs are inline asm: their completion is waited for explicitly,
+    // before the barrier after which the tile is read.
+    auto dma_wait_sync = [&]() __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+
+    // ---- staging of the plain loop: two register sets, two LDS stages ----
     int goffk[LOADS], goffv[LOADS];   // lane byte offsets of its chunks in a K / V tile
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
@@ -195,30 +239,6 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
         goffk[j] = ((sl / CPR) * kss + 8 * (sl % CPR)) * (int)sizeof(T);
         goffv[j] = ((sl / CPR) * vss + 8 * (sl % CPR)) * (int)sizeof(T);
     }
-    auto gload = [&](int kt) __attribute__((always_inline)) {
-        const auto kr = bwd_rows_rsrc<T, D>(kg, kt * BN, S, kss);
-        const auto vr = bwd_rows_rsrc<T, D>(vg, kt * BN, S, vss);
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j)
-            if (!PARTIAL || j * kBwdThreads + tid < TL::CHUNKS) {
-                kreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(kr, goffk[j], 0, 0));
-                vreg[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(vr, goffv[j], 0, 0));
-            }
-    };
-    auto swrite = [&](int st) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < LOADS; ++j) {
-            const int sl = j * kBwdThreads + tid;
-            if (!PARTIAL || sl < TL::CHUNKS) {
-                const int row = sl / CPR, pc = sl % CPR;
-                *(u32x4_t *)(&smem[st][0][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = kreg[j];
-                *(u32x4_t *)(&smem[st][1][row * D + 8 * (pc ^ swz_v<CPR>(row))]) = kreg[j];
-                *(u32x4_t *)(&smem[st][2][row * D + 8 * (pc ^ swz_k<CPR>(row))]) = vreg[j];
-            }
-        }
-    };
-
-    // ---- staging of the plain loop: two register sets, two LDS stages ----
     u32x4_t kreg2[2][LOADS], vreg2[2][LOADS];
     auto gload2 = [&](int kt, auto set_c) __attribute__((always_inline)) {
         constexpr int SET = decltype(set_c)::value;
@@ -282,27 +302,27 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
     };
 
     // One loop over the key tiles.  PASS 0: D_n; PASS 1: dS and dQ.  Software
-    // pipelined by one tile: step kt issues the S^T, dP^T MFMAs of tile kt+1
-    // one by one, each followed by a share of tile kt's softmax VALU (P, dS),
-    // with the MFMA fragments read RING MFMAs ahead; then the dQ MFMAs of
-    // tile kt, then tile kt+2 goes from registers to LDS and tile kt+3 is
-    // loaded.  One barrier per tile.
+    // pipelined by one tile: step kt starts the DMAs of tile kt+2, issues the
+    // S^T, dP^T MFMAs of tile kt+1 one by one, each followed by a share of
+    // tile kt's softmax VALU (P, dS), then the dQ MFMAs of tile kt, all MFMA
+    // fragments read RING MFMAs ahead through one ring.  One barrier per
+    // tile, after the wait for the DMAs.
     constexpr int RING = 4;
     constexpr int NUNIT = 16;   // softmax units of a tile: (kb, register pair)
     auto key_loop = [&](auto pass_c) __attribute__((always_inline)) {
         constexpr int PASS = decltype(pass_c)::value;
-        gload(0);
-        swrite(0);
-        gload(min(1, nt - 1));
-        swrite(1);
-        gload(min(2, nt - 1));
-        __syncthreads();
+        dma_tile(0);
+        if (nt > 1) dma_tile(1);
+        dma_wait_sync();
         f32x16_t s0[2], dp0[2], s1[2], dp1[2];
         if (wave_active) sd_tile(s0, dp0, 0);
 
         auto step = [&](int kt, f32x16_t (&sc)[2], f32x16_t (&dpc)[2], f32x16_t (&sn)[2], f32x16_t (&dpn)[2])
                         __attribute__((always_inline)) {
             const int st = kt % 3, st1 = (kt + 1) % 3;
+            // tile kt+2 into the stage of tile kt-1, which every wave finished
+            // reading before the last barrier
+            if (kt + 2 < nt) dma_tile(kt + 2);
             const int kbase = kt * BN;
             const bool wave_needed = wave_active && (!CAUSAL || kbase <= q0w + 31);
             // Two copies of the tile's work, with and without the mask (a
@@ -314,6 +334,19 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                 constexpr bool MASK = decltype(mask_c)::value;
                 const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
                 uint32_t dsk[2][8];
+                // One stream of fragments through the ring: the S^T, dP^T
+                // row fragments of tile kt+1, then (dQ pass) the transposed K
+                // fragments of tile kt, so the first dQ MFMAs find theirs read.
+                const T *Kv = smem[st][1];
+                constexpr int NQ = PASS == 1 ? 4 * NDB : 0;
+                static_assert(NSD % RING == 0, "the dQ MFMAs continue the ring");
+                // dQ MFMA m is (kb, cc, db) = (m / (2 NDB), (m / NDB) % 2, m % NDB)
+                auto kt_frag = [&](int m) __attribute__((always_inline)) {
+                    return bwd_tr_frag<T, D>(Kv, m / (2 * NDB), (m / NDB) & 1, m % NDB, vrow0, vcol0);
+                };
+                auto next_frag = [&](int n) __attribute__((always_inline)) {
+                    return n < NSD ? sd_frag(st1, n) : kt_frag(n - NSD);
+                };
                 frag ring[RING];
 #pragma unroll
                 for (int i = 0; i < RING; ++i) ring[i] = sd_frag(st1, i);
@@ -321,7 +354,7 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                 for (int m = 0; m < NSD; ++m) {
                     __builtin_amdgcn_sched_barrier(0);
                     sd_mma(sn, dpn, m, ring[m % RING]);
-                    if (m + RING < NSD) ring[m % RING] = sd_frag(st1, m + RING);
+                    if (m + RING < NSD + NQ) ring[m % RING] = next_frag(m + RING);
                     // softmax units of tile kt behind this MFMA
 #pragma unroll
                     for (int u = (m * NUNIT) / NSD; u < ((m + 1) * NUNIT) / NSD; ++u) {
@@ -343,33 +376,24 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if (PASS == 1) {
-                    // dQ^T += K^T dS^T over the 4 blocks of 16 keys: MFMA m is
-                    // (kb, cc, db) = (m / (2 NDB), (m / NDB) % 2, m % NDB), its
-                    // transposed K fragment read RING MFMAs ahead
-                    const T *Kv = smem[st][1];
-                    constexpr int NQ = 4 * NDB;
-                    auto kt_frag = [&](int m) __attribute__((always_inline)) {
-                        return bwd_tr_frag<T, D>(Kv, m / (2 * NDB), (m / NDB) & 1, m % NDB, vrow0, vcol0);
-                    };
-                    frag qring[RING];
-#pragma unroll
-                    for (int i = 0; i < RING; ++i) qring[i] = kt_frag(i);
+                    // dQ^T += K^T dS^T over the 4 blocks of 16 keys, the
+                    // transposed K fragments continuing the ring
 #pragma unroll
                     for (int m = 0; m < NQ; ++m) {
+                        __builtin_amdgcn_sched_barrier(0);
                         const int kb = m / (2 * NDB), cc = (m / NDB) & 1, db = m % NDB;
                         const u32x4_t bw = {dsk[kb][4 * cc], dsk[kb][4 * cc + 1], dsk[kb][4 * cc + 2], dsk[kb][4 * cc + 3]};
-                        acc[db] = E::mma(qring[m % RING], __builtin_bit_cast(frag, bw), acc[db]);
-                        if (m + RING < NQ) qring[m % RING] = kt_frag(m + RING);
+                        acc[db] = E::mma(ring[m % RING], __builtin_bit_cast(frag, bw), acc[db]);
+                        if (m + RING < NQ) ring[m % RING] = kt_frag(m + RING);
                     }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             };
             if (wave_needed) {
                 if (need_mask) work(std::true_type{});
                 else work(std::false_type{});
             }
-            if (kt + 2 < nt) swrite((kt + 2) % 3);
-            if (kt + 3 < nt) gload(kt + 3);
-            __syncthreads();
+            dma_wait_sync();
         };
         for (int kt = 0; kt < nt; kt += 2) {
             step(kt, s0, dp0, s1, dp1);
