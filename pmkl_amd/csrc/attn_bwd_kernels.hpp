@@ -67,9 +67,10 @@ template <int D> constexpr int bwd_waves_dq() { return D >= 128 ? 4 : 8; }
 template <int D> constexpr int bwd_waves_dkdv() { return D >= 128 ? 4 : 8; }
 
 // 16-byte chunk (logical chunk pc of row `row`) staging of a 64-row tile:
-// loads go to registers ahead of use (the dQ pass two tiles ahead, the dK/dV
-// pass one), LDS writes place the chunk at its swizzled position in each
-// layout the tensor is read with.
+// loads go to registers ahead of use (the dK/dV pass one tile ahead, the
+// dQ pass's plain loop below head_dim 128), LDS writes place the chunk at its
+// swizzled position in each layout the tensor is read with; the dQ pass at
+// head_dim 128 moves the chunks by LDS DMA instead.
 template <typename T, int D, int NW_>
 struct BwdTile {
     static constexpr int NW = NW_;
