@@ -351,28 +351,31 @@ __global__ __launch_bounds__(bwd_waves_dq<D>() * 64, 1) void attn_bwd_dq_kernel(
                 frag ring[RING];
 #pragma unroll
                 for (int i = 0; i < RING; ++i) ring[i] = sd_frag(st1, i);
+                // Softmax unit u of tile kt (registers 2u, 2u+1 of block u / 8)
+                // in two halves, one behind each MFMA: the exponentials behind
+                // MFMA 2u, the products behind MFMA 2u+1, so no two MFMAs issue
+                // back to back and the exponentials' latency passes under an
+                // MFMA.
+                static_assert(2 * NUNIT == NSD, "one half-unit per MFMA");
+                float pv[2];
 #pragma unroll
                 for (int m = 0; m < NSD; ++m) {
                     __builtin_amdgcn_sched_barrier(0);
                     sd_mma(sn, dpn, m, ring[m % RING]);
                     if (m + RING < NSD + NQ) ring[m % RING] = next_frag(m + RING);
-                    // softmax units of tile kt behind this MFMA
-#pragma unroll
-                    for (int u = (m * NUNIT) / NSD; u < ((m + 1) * NUNIT) / NSD; ++u) {
-                        const int kb = u >> 3, r = 2 * (u & 7);
-                        float pv[2];
+                    const int u = m >> 1, kb = u >> 3, r = 2 * (u & 7);
+                    if ((m & 1) == 0) {
 #pragma unroll
                         for (int e = 0; e < 2; ++e) {
                             const int key = kbase + 32 * kb + 16 * hi + r + e;
                             const float sv = MASK && key > lim ? -INFINITY : sc[kb][r + e];
                             pv[e] = fast_exp2(__builtin_fmaf(sv, c, -lse2));
                         }
-                        if (PASS == 0) {
-                            drow_part = __builtin_fmaf(pv[0], dpc[kb][r], drow_part);
-                            drow_part = __builtin_fmaf(pv[1], dpc[kb][r + 1], drow_part);
-                        } else {
-                            dsk[kb][r >> 1] = E::pack2(pv[0] * (dpc[kb][r] - drow), pv[1] * (dpc[kb][r + 1] - drow));
-                        }
+                    } else if (PASS == 0) {
+                        drow_part = __builtin_fmaf(pv[0], dpc[kb][r], drow_part);
+                        drow_part = __builtin_fmaf(pv[1], dpc[kb][r + 1], drow_part);
+                    } else {
+                        dsk[kb][r >> 1] = E::pack2(pv[0] * (dpc[kb][r] - drow), pv[1] * (dpc[kb][r + 1] - drow));
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
