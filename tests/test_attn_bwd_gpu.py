@@ -121,13 +121,20 @@ def test_bwd_small_shapes_vs_oracle(device, dtype, D, causal):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
-def test_bwd_with_forward_output(device, dtype):
-    """Row terms from <dout, O> instead of the extra pass over the keys."""
+@pytest.mark.parametrize("D", [64, 128])
+def test_bwd_with_forward_output(device, dtype, D):
+    """Row terms from <dout, O> instead of the extra pass over the keys
+    (head_dim 128: the pipelined dQ loop with DMA staging runs its second
+    pass only).  Not at S = 1: with one visible key per row the exact dq is 0,
+    and <dout, O> over the rounded O leaves rounding noise where the pass over
+    the keys cancels exactly (why the reference operator's API, which takes
+    no O, is served by that pass)."""
     for causal in (True, False):
-        tag = f"bwd with O {dtype} causal={causal}"
-        _say(f"case {tag}")
-        got, ref, fl = _run(2, 2, 300, 64, dtype, causal, seed=400, with_o=True)
-        _check(got, ref, dtype, tag, fl)
+        for S in ((300,) if D == 64 else (63, 300)):
+            tag = f"bwd with O {dtype} D={D} S={S} causal={causal}"
+            _say(f"case {tag}")
+            got, ref, fl = _run(2, 2, S, D, dtype, causal, seed=400 + S, with_o=True)
+            _check(got, ref, dtype, tag, fl)
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
