@@ -1,6 +1,8 @@
 """Scans the generated gfx950 code of the 64-row kernel (every instantiation of
-one translation unit, compiled here with the library's flags) for hazards that
-inline assembly hides from the compiler and that tests show only by chance:
+one translation unit, compiled here with the library's flags), and of the
+head_dim-128 backward kernels (whose dQ pass stages K/V by the same kind of
+LDS-DMA block), for hazards that inline assembly hides from the compiler and
+that tests show only by chance:
 
 * SCC across the LDS-DMA block: the block forms M0 with s_add_u32, which writes
   SCC.  An SCC reader whose last SCC writer comes before such a block reads the
@@ -31,13 +33,25 @@ SCC_WRITE = re.compile(
 SCC_READ = re.compile(r"^(s_cselect|s_cbranch_scc|s_addc_u32|s_subb_u32|s_cmov)")
 
 
-def _asm(tmp_path: Path) -> list[str]:
+# The head_dim-128 backward kernels, instantiated explicitly.
+BWD_TU = """#include <hip/hip_runtime.h>
+#include "attn_bwd_kernels.hpp"
+namespace pmkl_amd {
+template __global__ void attn_bwd_dq_kernel<__bf16, 128, true>(BwdParams);
+template __global__ void attn_bwd_dq_kernel<__bf16, 128, false>(BwdParams);
+template __global__ void attn_bwd_dq_kernel<_Float16, 128, true>(BwdParams);
+template __global__ void attn_bwd_dkdv_kernel<__bf16, 128, true>(BwdParams);
+}
+"""
+
+
+def _asm(tmp_path: Path, tu: Path = TU) -> list[str]:
     if not Path(HIPCC).exists():
         pytest.skip("hipcc not available")
-    out = tmp_path / "w64.s"
+    out = tmp_path / "k.s"
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
            "-packed-fp32-ops", "-I", str(ROOT / "include"), "-I", str(ROOT / "pmkl_amd" / "csrc"),
-           str(TU), "--cuda-device-only", "-S", "-o", str(out)]
+           str(tu), "--cuda-device-only", "-S", "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     lines = []
     for raw in out.read_text().splitlines():
@@ -52,12 +66,20 @@ def asm_lines(tmp_path_factory):
     return _asm(tmp_path_factory.mktemp("isa"))
 
 
+@pytest.fixture(scope="module")
+def bwd_asm_lines(tmp_path_factory):
+    d = tmp_path_factory.mktemp("isa_bwd")
+    tu = d / "bwd.hip"
+    tu.write_text(BWD_TU)
+    return _asm(d, tu)
+
+
 def test_kernels_compiled(asm_lines):
     kernels = [l for l in asm_lines if re.match(r"^_ZN8pmkl_amd19attn_fwd_w64_kernel.*:$", l)]
     assert len(kernels) >= 6, kernels
 
 
-def test_no_scc_read_across_lds_dma(asm_lines):
+def _scc_sites(asm_lines):
     bad = []
     writer_before_dma = False   # the last SCC writer precedes a DMA block (no writer since)
     for i, l in enumerate(asm_lines):
@@ -72,6 +94,22 @@ def test_no_scc_read_across_lds_dma(asm_lines):
             bad.append((i, l))
         if SCC_WRITE.match(op):
             writer_before_dma = False
+    return bad
+
+
+def test_no_scc_read_across_lds_dma(asm_lines):
+    bad = _scc_sites(asm_lines)
+    assert not bad, bad[:5]
+
+
+def test_backward_kernels_compiled_with_lds_dma(bwd_asm_lines):
+    kernels = [l for l in bwd_asm_lines if re.match(r"^_ZN8pmkl_amd(18attn_bwd_dq|20attn_bwd_dkdv)_kernel.*:$", l)]
+    assert len(kernels) == 4, kernels
+    assert sum(1 for l in bwd_asm_lines if l.startswith("buffer_load_dwordx4") and l.endswith(" lds")) > 0
+
+
+def test_no_scc_read_across_lds_dma_backward(bwd_asm_lines):
+    bad = _scc_sites(bwd_asm_lines)
     assert not bad, bad[:5]
 
 
