@@ -4,7 +4,8 @@ random (S from 1 to 700, log-uniform, so that ragged tiles, single tiles and
 multi-item workgroups all occur), every head_dim and dtype, causal or not.
 Each case runs the forward against the float64 forward oracle
 (tests/parity.py bounds) and then the backward, fed with that forward's m and
-l, against the float64 backward oracle (bounds of test_attn_bwd_gpu.py).
+l, against the float64 backward oracle (bounds of test_attn_bwd_gpu.py),
+without the forward's output and (S > 1) with it.
 The case list is a pure function of the seed, so a failure names a case that
 reruns identically.
 """
@@ -58,6 +59,13 @@ def test_random_shape_forward_and_backward(device, case):
     ref = oracle.attn_bwd(r(q), r(k), r(v), r(do), mn, ln, causal=causal)
     fl = _term_floors(r(q), r(k), r(v), r(do), mn, ln, causal) if dtype == "fp32" else (0.0, 0.0, 0.0)
     _say(f"  {_check([r(dq), r(dk), r(dv)], ref, dtype, tag, fl)}")
+    # The autograd path's call: row terms from <dout, O> (not at S = 1, where
+    # every row has one visible key and the exact dq is 0: see
+    # test_attn_bwd_gpu.test_bwd_with_forward_output).
+    if S > 1:
+        dq, dk, dv = pmkl_amd.attn_bwd(do.to("cuda:0"), qd, kd, vd, m, l, is_causal=causal, out=o)
+        torch.cuda.synchronize()
+        _say(f"  with O {_check([r(dq), r(dk), r(dv)], ref, dtype, tag + ' with O', fl)}")
 
 
 N_MANY = 12
